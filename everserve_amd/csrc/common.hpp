@@ -1,0 +1,78 @@
+// Shared pieces of libeverserve_mi355x: the per-thread error message, HIP error checks and an
+// exact 32-bit divider for index arithmetic inside kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "everserve_mi355x.h"
+
+namespace evs {
+
+// The message evs_last_error() returns; one per calling thread.
+void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+void clear_error();
+
+#define EVS_REQUIRE(cond, ...)        \
+  do {                                \
+    if (!(cond)) {                    \
+      ::evs::set_error(__VA_ARGS__);  \
+      return EVS_EINVAL;              \
+    }                                 \
+  } while (0)
+
+#define EVS_HIP(call)                                                                     \
+  do {                                                                                    \
+    hipError_t evs_rc_ = (call);                                                          \
+    if (evs_rc_ != hipSuccess) {                                                          \
+      ::evs::set_error("%s failed: %s (%d)", #call, hipGetErrorString(evs_rc_),          \
+                       static_cast<int>(evs_rc_));                                        \
+      return EVS_EHIP;                                                                    \
+    }                                                                                     \
+  } while (0)
+
+// The launch's own error (bad configuration, missing code object) right after enqueueing it.
+#define EVS_LAUNCHED(what)                                                                \
+  do {                                                                                    \
+    hipError_t evs_rc_ = hipGetLastError();                                               \
+    if (evs_rc_ != hipSuccess) {                                                          \
+      ::evs::set_error("%s launch failed: %s (%d)", what, hipGetErrorString(evs_rc_),    \
+                       static_cast<int>(evs_rc_));                                        \
+      return EVS_EHIP;                                                                    \
+    }                                                                                     \
+  } while (0)
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// q = n / d and r = n % d for 0 <= n < 2^31 and 1 <= d < 2^31 with one multiply-high: the
+// round-up method (Granlund and Montgomery, "Division by invariant integers using
+// multiplication", 1994). m = floor(2^(32+s) / d) + 1 with s = ceil(log2 d) makes
+// floor(n * m / 2^(32+s)) == floor(n / d) for every n < 2^31.
+struct FastDiv {
+  uint32_t d;
+  uint32_t m;
+  uint32_t s;
+
+  __host__ __device__ FastDiv() : d(1), m(0), s(0) {}
+  explicit FastDiv(uint32_t divisor) : d(divisor) {
+    s = 0;
+    while ((uint64_t{1} << s) < d) ++s;
+    m = static_cast<uint32_t>(((uint64_t{1} << (32 + s)) + d - 1) / d - (uint64_t{1} << 32));
+    // d a power of two: m == 0 and the quotient is a plain shift
+  }
+  __host__ __device__ __forceinline__ uint32_t div(uint32_t n) const {
+    const uint32_t hi = static_cast<uint32_t>((static_cast<uint64_t>(n) * m) >> 32);
+    return (hi + n) >> s;
+  }
+  __host__ __device__ __forceinline__ void divmod(uint32_t n, uint32_t& q, uint32_t& r) const {
+    q = div(n);
+    r = n - q * d;
+  }
+};
+
+inline bool aligned16(int64_t v) { return (v & 15) == 0; }
+
+}  // namespace evs

@@ -1,0 +1,295 @@
+// The reduction stage of the failure-detecting all-reduce, over member buffers in this GPU's HBM.
+//
+// Member r's bf16 payload sits at bufs[r]; it is ready when flags[r] carries the call's epoch
+// (the producer writes the payload, then releases the flag). The sum runs in the member order
+// the device array `order` lists ([count, rows...]), in fp32 from 0.0f, rounded once to bf16 by
+// torch's rule: core/csrc/slot.cu:118-123,203-223 and core/everserve/reference/arith/ops.py:63-73.
+// Floating-point addition is not associative, so the order is part of the result.
+//
+// Waiting is bounded. Wave 0 of every workgroup polls the flags, one lane per member, with
+// system-scope loads (a peer's stores over xGMI, or the host's, land behind this GPU's caches),
+// and combines the lanes with a ballot. Every 32 polls it reads the wall clock and lane 0 reads
+// the ABORT control word. The wait ends when every flag has arrived, when ABORT is set, when
+// another workgroup of the same call gave up, or when the hard timeout passes; a member still
+// missing then contributes zeros, as the reference's aborted reads do (slot.cu:148). Past the
+// BOUND control word (ns, 0 = off) the workgroup writes the rows it still waits for into LATE,
+// and the last workgroup that named clears LATE once its wait is over (slot.cu:29-40,174-214).
+//
+// The call's outcome is one word, state[0] = (epoch << 16) | (reason << 8) | late rows, written by
+// the last workgroup to finish. The counters behind it (state[1..3]) return to zero at the end of
+// every call, so the launch needs no memset and a captured graph can replay it.
+
+#include "common.hpp"
+
+namespace evs {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kMaxRows = EVS_MAX_ROWS;
+constexpr int kVpt = 2;            // 8-element vectors per thread per pass
+constexpr int kMaxBlocks = 1024;   // resident at once on 256 CUs: every workgroup polls once
+constexpr int kPollsPerCheck = 32; // flag polls between clock and ABORT reads
+constexpr int kBadOrder = 4;       // reason bit: `order` named a row outside [0, MAX_ROWS)
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+struct ReduceArgs {
+  const int64_t* bufs;
+  const uint64_t* flags;
+  const int32_t* order;
+  uint16_t* out;
+  int64_t n;
+  int64_t nvec;         // 8-element vectors when the vector path is on, else 0
+  uint64_t epoch;
+  int64_t timeout_ticks;
+  int64_t clock_khz;
+  uint64_t max_polls;   // a bound on polls that holds even if the clock stood still
+  int64_t* ctrl;        // may be null: no abort word, no late word
+  uint64_t* state;
+};
+
+__device__ __forceinline__ uint64_t load_system(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+__device__ __forceinline__ void store_system(int64_t* p, int64_t v) {
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), static_cast<uint64_t>(v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t bits16) {
+  return __uint_as_float(bits16 << 16);
+}
+
+// torch's float -> bfloat16: round to nearest even on the bit pattern, any NaN to 0x7FC0.
+__device__ __forceinline__ uint32_t f32_to_bf16(float f) {
+  const uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+__global__ __launch_bounds__(kThreads) void local_reduce(ReduceArgs a) {
+  __shared__ const uint16_t* s_src[kMaxRows];  // member in order position q, or null: missing
+  __shared__ int s_count;
+  __shared__ int s_vectors;                      // every member buffer 16-byte aligned
+  __shared__ uint32_t s_outcome;                 // reason << 8 | late rows
+
+  const int tid = threadIdx.x;
+  if (tid < 64) {
+    const int lane = tid;
+    int count = a.order[0];
+    count = count < 0 ? 0 : (count > kMaxRows ? kMaxRows : count);
+    const int row = lane < count ? a.order[1 + lane] : -1;
+    const bool listed = lane < count;
+    const bool valid = listed && row >= 0 && row < kMaxRows;
+    uint32_t reason = __ballot(listed && !valid) ? kBadOrder : 0;
+
+    const int64_t t0 = wall_clock64();
+    bool named = false;
+    uint32_t late_rows = 0;
+    uint64_t missing = 0;
+    for (uint64_t poll = 0;; ++poll) {
+      const bool ready = !valid || load_system(a.flags + row) == a.epoch;
+      missing = __ballot(!ready);
+      if (missing == 0) break;
+      if (poll % kPollsPerCheck == kPollsPerCheck - 1) {
+        const int64_t waited = wall_clock64() - t0;
+        uint64_t abort = 0, given_up = 0, bound_ns = 0;
+        if (lane == 0) {
+          if (a.ctrl != nullptr) {
+            abort = load_system(reinterpret_cast<const uint64_t*>(a.ctrl + EVS_ABORT));
+            bound_ns = load_system(reinterpret_cast<const uint64_t*>(a.ctrl + EVS_BOUND));
+          }
+          given_up = __hip_atomic_load(a.state + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >> 8;
+        }
+        abort = __shfl(abort, 0);
+        given_up = __shfl(given_up, 0);
+        bound_ns = __shfl(bound_ns, 0);
+        // rows this workgroup still waits for
+        const uint32_t mine = (missing >> lane) & 1 ? (1u << row) : 0u;
+        uint32_t rows = mine;
+        for (int q = 1; q < kMaxRows; q <<= 1) rows |= __shfl_xor(rows, q);
+        late_rows = rows;
+        const int64_t waited_ns = waited * 1000000 / a.clock_khz;
+        if (a.ctrl != nullptr && static_cast<int64_t>(bound_ns) > 0 &&
+            waited_ns > static_cast<int64_t>(bound_ns)) {
+          if (lane == 0) {
+            if (!named)
+              __hip_atomic_fetch_add(a.state + 3, uint64_t{1}, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
+            // every check: another workgroup's clear may have raced this one's write
+            store_system(a.ctrl + EVS_LATE, static_cast<int64_t>(late_rows));
+          }
+          named = true;
+        }
+        if (abort != 0) {
+          reason |= EVS_REDUCE_ABORTED;
+          break;
+        }
+        if (given_up != 0) {
+          reason |= static_cast<uint32_t>(given_up) & (EVS_REDUCE_ABORTED | EVS_REDUCE_TIMED_OUT);
+          break;
+        }
+        if (waited > a.timeout_ticks || poll >= a.max_polls) {
+          reason |= EVS_REDUCE_TIMED_OUT;
+          break;
+        }
+      }
+      __builtin_amdgcn_s_sleep(2);
+    }
+    if (missing == 0) late_rows = 0;
+    if (named && lane == 0) {
+      // the wait is over; the last workgroup that named clears the word
+      if (__hip_atomic_fetch_add(a.state + 3, ~uint64_t{0}, __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT) == 1)
+        store_system(a.ctrl + EVS_LATE, 0);
+    }
+    const int64_t addr = valid ? a.bufs[row] : 0;
+    const bool unaligned = __ballot((addr & 15) != 0) != 0;
+    if (lane < kMaxRows) {
+      const bool have = valid && !((missing >> lane) & 1);
+      s_src[lane] = have ? reinterpret_cast<const uint16_t*>(addr) : nullptr;
+    }
+    if (lane == 0) {
+      s_count = count;
+      s_vectors = !unaligned;
+      s_outcome = (reason << 8) | late_rows;
+    }
+  }
+  __syncthreads();
+  // the flags were read with relaxed loads: order the payload reads after them
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+
+  const int count = s_count;
+  const int64_t nvec = s_vectors ? a.nvec : 0;
+  const uint16_t* src[kMaxRows];
+#pragma unroll
+  for (int q = 0; q < kMaxRows; q++) src[q] = q < count ? s_src[q] : nullptr;
+
+  // vectors of 8 elements: one 16-byte load per member
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads * kVpt;
+  for (int64_t v0 = static_cast<int64_t>(blockIdx.x) * kThreads * kVpt + tid; v0 < nvec;
+       v0 += stride) {
+    u32x4 x[kVpt][kMaxRows];
+#pragma unroll
+    for (int i = 0; i < kVpt; i++) {
+      const int64_t v = v0 + static_cast<int64_t>(i) * kThreads;
+#pragma unroll
+      for (int q = 0; q < kMaxRows; q++) {
+        x[i][q] = u32x4{0u, 0u, 0u, 0u};
+        if (v < nvec && src[q] != nullptr)
+          x[i][q] = *reinterpret_cast<const u32x4*>(src[q] + v * 8);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kVpt; i++) {
+      const int64_t v = v0 + static_cast<int64_t>(i) * kThreads;
+      if (v >= nvec) continue;
+      float acc[8];
+#pragma unroll
+      for (int e = 0; e < 8; e++) acc[e] = 0.0f;
+#pragma unroll
+      for (int q = 0; q < kMaxRows; q++) {
+        if (q >= count) continue;
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+          acc[2 * w] += bf16_to_f32(x[i][q][w] & 0xffffu);
+          acc[2 * w + 1] += bf16_to_f32(x[i][q][w] >> 16);
+        }
+      }
+      u32x4 y;
+#pragma unroll
+      for (int w = 0; w < 4; w++) y[w] = f32_to_bf16(acc[2 * w]) | (f32_to_bf16(acc[2 * w + 1]) << 16);
+      *reinterpret_cast<u32x4*>(a.out + v * 8) = y;
+    }
+  }
+  // the elements the vectors do not cover: a tail of fewer than 8, or all of them when a buffer
+  // is not 16-byte aligned
+  const int64_t first = nvec * 8;
+  for (int64_t e = first + static_cast<int64_t>(blockIdx.x) * kThreads + tid; e < a.n;
+       e += static_cast<int64_t>(gridDim.x) * kThreads) {
+    float acc = 0.0f;
+    for (int q = 0; q < count; q++) acc += src[q] != nullptr ? bf16_to_f32(src[q][e]) : 0.0f;
+    a.out[e] = static_cast<uint16_t>(f32_to_bf16(acc));
+  }
+
+  if (tid == 0) {
+    const uint32_t outcome = s_outcome;
+    if (outcome != 0)
+      __hip_atomic_fetch_or(a.state + 2, static_cast<uint64_t>(outcome), __ATOMIC_RELAXED,
+                            __HIP_MEMORY_SCOPE_AGENT);
+    const uint64_t done = __hip_atomic_fetch_add(a.state + 1, uint64_t{1}, __ATOMIC_ACQ_REL,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+    if (done == gridDim.x - 1) {
+      // the last workgroup: every other one's outcome is in state[2]
+      const uint64_t all = __hip_atomic_exchange(a.state + 2, uint64_t{0}, __ATOMIC_ACQ_REL,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(a.state + 1, uint64_t{0}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(a.state + 0, (a.epoch << 16) | (all & 0xffffu), __ATOMIC_RELEASE,
+                         __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+  }
+}
+
+int64_t g_clock_khz[64];
+
+int clock_khz(int64_t* khz) {
+  int dev = 0;
+  EVS_HIP(hipGetDevice(&dev));
+  EVS_REQUIRE(dev >= 0 && dev < 64, "device %d out of range", dev);
+  if (g_clock_khz[dev] == 0) {
+    int rate = 0;
+    EVS_HIP(hipDeviceGetAttribute(&rate, hipDeviceAttributeWallClockRate, dev));
+    EVS_REQUIRE(rate > 0, "device %d reports no wall clock rate", dev);
+    g_clock_khz[dev] = rate;
+  }
+  *khz = g_clock_khz[dev];
+  return EVS_OK;
+}
+
+}  // namespace
+
+int wall_clock_khz(int64_t* khz) { return clock_khz(khz); }
+
+}  // namespace evs
+
+extern "C" int evs_local_reduce(const int64_t* bufs, const uint64_t* flags, const int32_t* order,
+                                void* out, int64_t n, uint64_t epoch, int64_t timeout_ns,
+                                int64_t* ctrl, uint64_t* state, void* stream) {
+  evs::clear_error();
+  EVS_REQUIRE(bufs != nullptr && flags != nullptr && order != nullptr && state != nullptr,
+              "evs_local_reduce: null pointer");
+  EVS_REQUIRE(n >= 0, "evs_local_reduce: negative element count");
+  EVS_REQUIRE(n == 0 || out != nullptr, "evs_local_reduce: null output");
+  EVS_REQUIRE((reinterpret_cast<int64_t>(out) & 1) == 0, "evs_local_reduce: unaligned output");
+  int64_t khz = 0;
+  int rc = evs::clock_khz(&khz);
+  if (rc != EVS_OK) return rc;
+  if (timeout_ns <= 0) timeout_ns = 1000000000;
+  EVS_REQUIRE(timeout_ns < (int64_t{1} << 50), "evs_local_reduce: timeout too large");
+  evs::ReduceArgs a{};
+  a.bufs = bufs;
+  a.flags = flags;
+  a.order = order;
+  a.out = static_cast<uint16_t*>(out);
+  a.n = n;
+  // the member buffers live in a device table the host does not read: the kernel checks their
+  // alignment itself and takes the element path when one is not 16-byte aligned
+  a.nvec = evs::aligned16(reinterpret_cast<int64_t>(out)) ? n / 8 : 0;
+  a.epoch = epoch;
+  a.timeout_ticks = timeout_ns / 1000 * khz / 1000;
+  a.clock_khz = khz;
+  a.max_polls = static_cast<uint64_t>(timeout_ns / 50) + 4096;
+  a.ctrl = ctrl;
+  a.state = state;
+  const int64_t per_block = static_cast<int64_t>(evs::kThreads) * evs::kVpt;
+  int64_t blocks = (a.nvec + per_block - 1) / per_block;
+  const int64_t tail_blocks = (n - a.nvec * 8 + evs::kThreads - 1) / evs::kThreads;
+  if (tail_blocks > blocks) blocks = tail_blocks;
+  if (blocks < 1) blocks = 1;
+  if (blocks > evs::kMaxBlocks) blocks = evs::kMaxBlocks;
+  hipLaunchKernelGGL(evs::local_reduce, dim3(static_cast<uint32_t>(blocks)), dim3(evs::kThreads),
+                     0, evs::as_stream(stream), a);
+  EVS_LAUNCHED("evs_local_reduce");
+  return EVS_OK;
+}

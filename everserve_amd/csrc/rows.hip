@@ -1,0 +1,288 @@
+// The step's KV rows between the paged cache and a staging buffer, on gfx950.
+//
+// Gather (the snapshot) reads each (layer, head slot, slot) K and V half-row out of a paged cache
+// and writes it into a buffer laid out [layers, heads, capacity, 2, head_dim]; scatter (the
+// restore) is its inverse. A cache layout is five strides (block, offset in block, head slot,
+// K-or-V, element), so the three paged layouts and strided views share one kernel
+// (core/everserve/state/kvcopy.py:105-116; the reference kernels are core/csrc/gather.cu:29-71).
+//
+// Work is cut into tiles of (one layer, TS consecutive slots, every held head). One workgroup of
+// 256 threads owns a tile: its first TS threads turn the tile's slot ids (or block ids) into byte
+// offsets inside a layer, the first H threads the head slots, both into LDS, so each moved word
+// costs two LDS reads and no 64-bit division. Each thread then moves VPT words at a time, every
+// load in flight before the first store. A word is 16 bytes when every half-row is contiguous
+// and 16-byte aligned on both sides (bf16 d=128: 16 words a half-row, fp8 d=128: 8), else one
+// element. Within a tile words are numbered so that a wave's 64 lanes cover whole half-rows of
+// consecutive heads of one slot: in the kv_first layout that reads a block's K (or V) as one
+// contiguous stream, and writes 256-byte runs into each head's rows.
+
+#include "common.hpp"
+
+namespace evs {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kVpt = 8;             // words per thread per pass, all loads issued before stores
+constexpr int kMaxTileSlots = 64;
+constexpr int kMaxHeads = 256;      // LDS table of head offsets
+
+enum Dir : int { kGather = 0, kScatter = 1 };
+enum Index : int { kBySlots = 0, kByBlocks = 1 };
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+struct RowsArgs {
+  const int64_t* layer_ptrs;  // device: each layer's cache base address
+  const int64_t* slots;       // kBySlots: device slot ids
+  const int32_t* blocks;      // kByBlocks: device block ids
+  const int64_t* heads;       // device head slots
+  char* rows;                 // the staging buffer, [L, H, cap, 2, d]
+  int64_t* slots_out;         // kByBlocks: the expanded slot ids, or null
+  int64_t n;                  // slots moved per layer
+  int64_t cap;                // staging capacity (rows per (layer, head))
+  int64_t half_bytes;         // d * elem
+  int64_t sb, so, sh, skv;    // cache strides in bytes: block, offset, head, K-or-V
+  int64_t sj;                 // cache bytes between consecutive words of a half-row
+  int64_t bs;                 // slots per block
+  int bs_shift;               // log2(bs) when bs is a power of two, else -1
+  int H;
+  int TS;                     // slots per tile
+  uint32_t tile_words;        // TS * H * 2 * W
+  FastDiv div_w;              // words per half-row
+  FastDiv div_h;              // held heads
+  FastDiv div_ts;             // slots per tile
+  FastDiv div_tiles;          // tiles per layer
+};
+
+template <typename T>
+__device__ __forceinline__ T load_word(const char* p) {
+  return *reinterpret_cast<const T*>(p);
+}
+
+template <typename T>
+__device__ __forceinline__ void store_word(char* p, T v) {
+  *reinterpret_cast<T*>(p) = v;
+}
+
+__device__ __forceinline__ int64_t block_of(int64_t s, const RowsArgs& a) {
+  return a.bs_shift >= 0 ? (s >> a.bs_shift) : s / a.bs;
+}
+
+__device__ __forceinline__ int64_t offset_in_block(int64_t s, const RowsArgs& a) {
+  return a.bs_shift >= 0 ? (s & (a.bs - 1)) : s % a.bs;
+}
+
+template <typename T, int D, int I>
+__global__ __launch_bounds__(kThreads) void move_rows(RowsArgs a) {
+  __shared__ int64_t s_slot[kMaxTileSlots];  // byte offset of a slot's row in a layer, -1: none
+  __shared__ int64_t s_head[kMaxHeads];      // byte offset of a head slot in a row group
+
+  uint32_t layer, tile;
+  a.div_tiles.divmod(blockIdx.x, layer, tile);
+  const int tid = threadIdx.x;
+  const int64_t t0 = static_cast<int64_t>(tile) * a.TS;
+
+  if (tid < a.TS) {
+    const int64_t t = t0 + tid;
+    int64_t off = -1;
+    if (t < a.n) {
+      int64_t s;
+      if (I == kByBlocks) {
+        const int64_t blk = a.blocks[a.bs_shift >= 0 ? (t >> a.bs_shift) : t / a.bs];
+        s = blk * a.bs + offset_in_block(t, a);
+        if (a.slots_out != nullptr && layer == 0) a.slots_out[t] = s;
+      } else {
+        s = a.slots[t];
+      }
+      // padding (a negative id): the gather reads slot 0, as the torch path does; the scatter
+      // writes nothing
+      if (s < 0) s = (D == kGather) ? 0 : -1;
+      if (s >= 0) off = block_of(s, a) * a.sb + offset_in_block(s, a) * a.so;
+    }
+    s_slot[tid] = off;
+  }
+  for (int h = tid; h < a.H; h += kThreads) s_head[h] = a.heads[h] * a.sh;
+  __syncthreads();
+
+  const char* cache_base = reinterpret_cast<const char*>(a.layer_ptrs[layer]);
+  char* cache_w = reinterpret_cast<char*>(a.layer_ptrs[layer]);
+  char* rows_l = a.rows + static_cast<int64_t>(layer) * a.H * a.cap * (2 * a.half_bytes);
+
+  for (uint32_t v0 = 0; v0 < a.tile_words; v0 += kThreads * kVpt) {
+    T w[kVpt];
+    int64_t cache_off[kVpt];
+    int64_t rows_off[kVpt];
+    bool live[kVpt];
+#pragma unroll
+    for (int i = 0; i < kVpt; i++) {
+      const uint32_t v = v0 + i * kThreads + tid;
+      // v = ((k * TS + tl) * H + h) * W + j
+      uint32_t q, j, q2, h, k, tl;
+      a.div_w.divmod(v, q, j);
+      a.div_h.divmod(q, q2, h);
+      a.div_ts.divmod(q2, k, tl);
+      const int64_t slot_off = v < a.tile_words ? s_slot[tl] : -1;
+      live[i] = slot_off >= 0;
+      cache_off[i] = slot_off + s_head[live[i] ? h : 0] + k * a.skv + j * a.sj;
+      rows_off[i] = (static_cast<int64_t>(h) * a.cap + t0 + tl) * (2 * a.half_bytes) +
+                    k * a.half_bytes + static_cast<int64_t>(j) * sizeof(T);
+    }
+#pragma unroll
+    for (int i = 0; i < kVpt; i++) {
+      if (!live[i]) continue;
+      w[i] = D == kGather ? load_word<T>(cache_base + cache_off[i])
+                          : load_word<T>(rows_l + rows_off[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < kVpt; i++) {
+      if (!live[i]) continue;
+      if (D == kGather)
+        store_word<T>(rows_l + rows_off[i], w[i]);
+      else
+        store_word<T>(cache_w + cache_off[i], w[i]);
+    }
+  }
+}
+
+struct RowsCall {
+  const int64_t* layer_ptrs;
+  int64_t L;
+  const int64_t* slots;
+  const int32_t* blocks;
+  int64_t n_index;  // slots, or blocks
+  const int64_t* heads;
+  int64_t H;
+  char* rows;
+  int64_t cap;
+  int64_t d;
+  int64_t bs;
+  const int64_t* strides;
+  int64_t elem;
+  int64_t* slots_out;
+  hipStream_t stream;
+};
+
+template <int D, int I, typename T>
+int launch_typed(RowsArgs a, int64_t L, uint32_t W, hipStream_t stream, const char* name) {
+  const int64_t target = static_cast<int64_t>(kThreads) * kVpt;
+  const int64_t per_slot = static_cast<int64_t>(a.H) * 2 * W;
+  int64_t ts = target / per_slot;
+  ts = ts < 1 ? 1 : (ts > kMaxTileSlots ? kMaxTileSlots : ts);
+  if (ts > a.n) ts = a.n;
+  const int64_t tiles = (a.n + ts - 1) / ts;
+  const int64_t grid = tiles * L;
+  EVS_REQUIRE(ts * per_slot < (int64_t{1} << 31), "%s: a tile of %lld words is too large", name,
+              static_cast<long long>(ts * per_slot));
+  EVS_REQUIRE(grid < (int64_t{1} << 31), "%s: %lld workgroups exceed the launch limit", name,
+              static_cast<long long>(grid));
+  a.TS = static_cast<int>(ts);
+  a.tile_words = static_cast<uint32_t>(ts * per_slot);
+  a.div_w = FastDiv(W);
+  a.div_h = FastDiv(static_cast<uint32_t>(a.H));
+  a.div_ts = FastDiv(static_cast<uint32_t>(ts));
+  a.div_tiles = FastDiv(static_cast<uint32_t>(tiles));
+  hipLaunchKernelGGL((move_rows<T, D, I>), dim3(static_cast<uint32_t>(grid)), dim3(kThreads), 0,
+                     stream, a);
+  EVS_LAUNCHED(name);
+  return EVS_OK;
+}
+
+template <int D, int I>
+int move(const RowsCall& c, const char* name) {
+  EVS_REQUIRE(c.strides != nullptr, "%s: a layout is five strides", name);
+  EVS_REQUIRE(c.elem == 1 || c.elem == 2 || c.elem == 4, "%s: unsupported element size %lld",
+              name, static_cast<long long>(c.elem));
+  EVS_REQUIRE(c.L >= 0 && c.n_index >= 0 && c.H >= 0, "%s: negative count", name);
+  EVS_REQUIRE(c.d >= 1 && c.bs >= 1, "%s: head_dim and block_size must be positive", name);
+  EVS_REQUIRE(c.H <= kMaxHeads, "%s: at most %d head slots per call, got %lld", name, kMaxHeads,
+              static_cast<long long>(c.H));
+  const int64_t n = I == kByBlocks ? c.n_index * c.bs : c.n_index;
+  EVS_REQUIRE(n <= c.cap, "%s: more slots (%lld) than the staging capacity (%lld)", name,
+              static_cast<long long>(n), static_cast<long long>(c.cap));
+  if (n == 0 || c.H == 0 || c.L == 0) return EVS_OK;
+  EVS_REQUIRE(c.layer_ptrs != nullptr && c.heads != nullptr && c.rows != nullptr,
+              "%s: null pointer", name);
+  EVS_REQUIRE(I == kByBlocks ? c.blocks != nullptr : c.slots != nullptr, "%s: null index", name);
+
+  const int64_t e = c.elem;
+  RowsArgs a{};
+  a.layer_ptrs = c.layer_ptrs;
+  a.slots = c.slots;
+  a.blocks = c.blocks;
+  a.heads = c.heads;
+  a.rows = c.rows;
+  a.slots_out = c.slots_out;
+  a.n = n;
+  a.cap = c.cap;
+  a.half_bytes = c.d * e;
+  a.sb = c.strides[0] * e;
+  a.so = c.strides[1] * e;
+  a.sh = c.strides[2] * e;
+  a.skv = c.strides[3] * e;
+  a.bs = c.bs;
+  a.bs_shift = -1;
+  if ((c.bs & (c.bs - 1)) == 0) {
+    int s = 0;
+    while ((int64_t{1} << s) < c.bs) ++s;
+    a.bs_shift = s;
+  }
+  a.H = static_cast<int>(c.H);
+
+  const bool vectors = c.strides[4] == 1 && aligned16(c.d * e) &&
+                       aligned16(reinterpret_cast<int64_t>(c.rows)) && aligned16(a.sb) &&
+                       aligned16(a.so) && aligned16(a.sh) && aligned16(a.skv);
+  if (vectors) {
+    a.sj = 16;
+    return launch_typed<D, I, u32x4>(a, c.L, static_cast<uint32_t>(c.d * e / 16), c.stream, name);
+  }
+  a.sj = c.strides[4] * e;
+  EVS_REQUIRE(c.d < (int64_t{1} << 24), "%s: head_dim too large", name);
+  switch (e) {
+    case 1:
+      return launch_typed<D, I, uint8_t>(a, c.L, static_cast<uint32_t>(c.d), c.stream, name);
+    case 2:
+      return launch_typed<D, I, uint16_t>(a, c.L, static_cast<uint32_t>(c.d), c.stream, name);
+    default:
+      return launch_typed<D, I, uint32_t>(a, c.L, static_cast<uint32_t>(c.d), c.stream, name);
+  }
+}
+
+}  // namespace
+}  // namespace evs
+
+extern "C" int evs_gather_rows(const int64_t* layer_ptrs, int64_t num_layers,
+                               const int64_t* slots, int64_t num_slots, const int64_t* heads,
+                               int64_t num_heads, void* out, int64_t capacity, int64_t head_dim,
+                               int64_t block_size, const int64_t* strides, int64_t elem_size,
+                               void* stream) {
+  evs::clear_error();
+  evs::RowsCall c{layer_ptrs, num_layers, slots, nullptr, num_slots, heads, num_heads,
+                  static_cast<char*>(out), capacity, head_dim, block_size, strides, elem_size,
+                  nullptr, evs::as_stream(stream)};
+  return evs::move<evs::kGather, evs::kBySlots>(c, "evs_gather_rows");
+}
+
+extern "C" int evs_gather_blocks(const int64_t* layer_ptrs, int64_t num_layers,
+                                 const int32_t* block_ids, int64_t num_blocks,
+                                 const int64_t* heads, int64_t num_heads, void* out,
+                                 int64_t capacity, int64_t head_dim, int64_t block_size,
+                                 const int64_t* strides, int64_t elem_size, int64_t* slots_out,
+                                 void* stream) {
+  evs::clear_error();
+  evs::RowsCall c{layer_ptrs, num_layers, nullptr, block_ids, num_blocks, heads, num_heads,
+                  static_cast<char*>(out), capacity, head_dim, block_size, strides, elem_size,
+                  slots_out, evs::as_stream(stream)};
+  return evs::move<evs::kGather, evs::kByBlocks>(c, "evs_gather_blocks");
+}
+
+extern "C" int evs_scatter_rows(const int64_t* layer_ptrs, int64_t num_layers,
+                                const int64_t* slots, int64_t num_slots, const int64_t* heads,
+                                int64_t num_heads, const void* in, int64_t capacity,
+                                int64_t head_dim, int64_t block_size, const int64_t* strides,
+                                int64_t elem_size, void* stream) {
+  evs::clear_error();
+  evs::RowsCall c{layer_ptrs, num_layers, slots, nullptr, num_slots, heads, num_heads,
+                  const_cast<char*>(static_cast<const char*>(in)), capacity, head_dim,
+                  block_size, strides, elem_size, nullptr, evs::as_stream(stream)};
+  return evs::move<evs::kScatter, evs::kBySlots>(c, "evs_scatter_rows");
+}

@@ -1,0 +1,494 @@
+"""The MI355X kernels: load the C-ABI library, say whether it is usable here, and expose it under
+the names and argument meanings of the reference's extension module ``everserve_kernels``.
+
+The library is ``libeverserve_mi355x.so``, built in tree by ``python -m everserve_amd.build``
+(hipcc for gfx950; no torch headers). Its C entry points are declared in
+``include/everserve_mi355x.h``. This module is the loader the reference's
+``core/everserve/kernels.py`` is, with the same contract (core/everserve/kernels.py:1-27,
+125-221):
+
+* a build is loaded only when its stamp (the sources by content, and the GPU architectures) is
+  this tree's and names this GPU: anything else raises :class:`KernelsUnavailable`, never a
+  silent fallback;
+* ``EVERSERVE_KERNELS_DIR`` names a build made elsewhere, loaded on the same terms;
+* ``EVERSERVE_KERNELS=torch`` is the only way to run without the kernels, and :func:`available`
+  then says False;
+* the architecture is the device's ``gcnArchName`` (``gfx950``), not a CUDA compute capability.
+
+:func:`load` returns a :class:`Kernels` object whose methods take the reference module's
+arguments (torch tensors for the device index arrays, integers for raw addresses) and enqueue on
+torch's current stream of the tensors' device, as the reference's ``gather_rows`` does
+(core/csrc/gather.cu:100-135).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import functools
+import json
+import logging
+import os
+from pathlib import Path
+from typing import Sequence
+
+log = logging.getLogger(__name__)
+
+NAME = "everserve_kernels"
+LIBRARY = "libeverserve_mi355x.so"
+PREBUILT_ENV = "EVERSERVE_KERNELS_DIR"
+"""A directory holding a build made ahead of time, loaded when its stamp is this tree's."""
+PATHS_ENV = "EVERSERVE_KERNELS"
+"""``torch`` to run on the torch paths without the kernels, by choice; anything else loads them."""
+STAMP = "stamp.json"
+HANDLE_BYTES = 64
+
+_PACKAGE = Path(__file__).resolve().parent
+
+EVS_OK = 0
+
+
+class KernelsUnavailable(RuntimeError):
+    """The kernels cannot be loaded here, and why: a wrong or stale build, no GPU."""
+
+
+class KernelError(RuntimeError):
+    """A kernel entry point refused its arguments or the HIP runtime failed; the library's message."""
+
+
+def stamp() -> dict[str, str]:
+    """What this tree's sources are, by content (the build records the same digest)."""
+    from everserve_amd import build
+
+    return {"sources": build.sources_digest()}
+
+
+def built_archs(archs: str) -> set[str]:
+    """The GPU architectures a build names (``"gfx942;gfx950"``: both)."""
+    return {a.strip().split(":")[0] for a in archs.replace(" ", ";").split(";") if a.strip()}
+
+
+def device_arch() -> str | None:
+    """This process's GPU architecture (``"gfx950"``), or None without a GPU."""
+    import torch
+
+    if not torch.cuda.is_available():
+        return None
+    return torch.cuda.get_device_properties(torch.cuda.current_device()).gcnArchName.split(":")[0]
+
+
+def _check_stamp(directory: Path) -> Path:
+    """The library in ``directory`` when its stamp is this tree's and names this GPU.
+
+    Raises:
+        KernelsUnavailable: no usable stamp, another tree's sources, another GPU, no library.
+    """
+    try:
+        theirs = json.loads((directory / STAMP).read_text())
+    except (OSError, ValueError) as e:
+        raise KernelsUnavailable(f"{directory}: no usable stamp ({e})") from e
+    ours = stamp()
+    if any(theirs.get(k) != v for k, v in ours.items()):
+        raise KernelsUnavailable(
+            f"{directory}: built against {theirs}, this tree is {ours}; "
+            "rebuild with python -m everserve_amd.build"
+        )
+    here = device_arch()
+    if here is not None and here not in built_archs(theirs.get("archs", "")):
+        raise KernelsUnavailable(
+            f"{directory}: built for {theirs.get('archs')}, this GPU is {here}"
+        )
+    so = directory / LIBRARY
+    if not so.is_file():
+        raise KernelsUnavailable(f"{directory}: stamped, but no {LIBRARY} in it")
+    return so
+
+
+def _prebuilt() -> Path | None:
+    """The library of the build ``EVERSERVE_KERNELS_DIR`` names; None when it names none.
+
+    Raises:
+        KernelsUnavailable: see :func:`_check_stamp`.
+    """
+    directory = os.environ.get(PREBUILT_ENV, "")
+    if not directory:
+        return None
+    return _check_stamp(Path(directory))
+
+
+def library_path() -> Path:
+    """The library this process loads: the named prebuilt, else the in-tree build.
+
+    The in-tree build is made here when there is none yet; an existing one whose stamp is not
+    this tree's is refused, not rebuilt around.
+    """
+    named = _prebuilt()
+    if named is not None:
+        return named
+    if not (_PACKAGE / LIBRARY).is_file():
+        from everserve_amd import build
+
+        log.info("no in-tree build of %s: building it now", LIBRARY)
+        build.build(_PACKAGE)
+    return _check_stamp(_PACKAGE)
+
+
+# (name, restype, argtypes) of every entry point in include/everserve_mi355x.h
+_I64, _P, _I32 = ctypes.c_int64, ctypes.c_void_p, ctypes.c_int
+_SIGNATURES: tuple[tuple[str, object, tuple], ...] = (
+    ("evs_last_error", ctypes.c_char_p, ()),
+    ("evs_layout_constants", _I32, (_P, _I64)),
+    ("evs_gather_rows", _I32, (_P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _P, _I64, _P)),
+    (
+        "evs_gather_blocks",
+        _I32,
+        (_P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _P, _I64, _P, _P),
+    ),
+    ("evs_scatter_rows", _I32, (_P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _P, _I64, _P)),
+    ("evs_local_reduce", _I32, (_P, _P, _P, _P, _I64, ctypes.c_uint64, _I64, _P, _P, _P)),
+    ("evs_slot_blocks", _I32, (_I64, _I64, _P)),
+    ("evs_host_register_mapped", _I32, (_P, _I64, _P)),
+    ("evs_host_unregister", _I32, (_P,)),
+    ("evs_host_alloc_mapped", _I32, (_I64, _P, _P)),
+    ("evs_host_free", _I32, (_P,)),
+    ("evs_device_alloc", _I32, (_I64, _P)),
+    ("evs_device_free", _I32, (_P,)),
+    ("evs_memset_async", _I32, (_P, _I64, _P)),
+    ("evs_copy_rows_async", _I32, (_P, _P, _I64, _I64, _I64, _P)),
+    ("evs_ipc_handle", _I32, (_P, _P, _I64)),
+    ("evs_ipc_open", _I32, (_P, _I64, _P)),
+    ("evs_ipc_close", _I32, (_P,)),
+    ("evs_wall_clock_khz", _I32, (_P,)),
+)
+ENTRY_POINTS = tuple(name for name, _, _ in _SIGNATURES)
+
+
+def open_library(path: Path | None = None) -> ctypes.CDLL:
+    """dlopen the library and declare every entry point's C signature. Needs no GPU.
+
+    torch is imported first so the library binds to the HIP runtime torch already loaded: one
+    runtime per process, so torch's stream handles are valid here.
+    """
+    import torch  # noqa: F401  (loads torch's HIP runtime before the library resolves it)
+
+    lib = ctypes.CDLL(str(path or library_path()))
+    for name, restype, argtypes in _SIGNATURES:
+        fn = getattr(lib, name)
+        fn.restype = restype
+        fn.argtypes = list(argtypes)
+    return lib
+
+
+def _stream_of(device) -> int:
+    import torch
+
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _device_ptr(t, what: str, dtype) -> int:
+    """A device tensor's address, after checking it is on the GPU and of ``dtype``."""
+    if not t.is_cuda:
+        raise RuntimeError(f"{what} must be on the device")
+    if t.dtype != dtype:
+        raise RuntimeError(f"{what} must be {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise RuntimeError(f"{what} must be contiguous")
+    return t.data_ptr()
+
+
+class Kernels:
+    """The loaded library under the reference module's names (core/csrc/kernels.cpp:9-31).
+
+    Attributes MAX_ROWS, CTRL_WORDS, ABORT, LATE and BOUND are the slot region's layout as the
+    library was built with it; ``core/everserve/comm/slotkernel.py:98-120`` compares its copy.
+    """
+
+    def __init__(self, lib: ctypes.CDLL, path: Path) -> None:
+        self._lib = lib
+        self.__file__ = str(path)
+        words = (ctypes.c_int64 * 5)()
+        self._check(lib.evs_layout_constants(words, 5))
+        self.MAX_ROWS, self.CTRL_WORDS, self.ABORT, self.LATE, self.BOUND = (int(w) for w in words)
+
+    def _check(self, rc: int) -> None:
+        if rc != EVS_OK:
+            raise KernelError(self._lib.evs_last_error().decode(errors="replace"))
+
+    # -------------------------------------------------------------- the step's KV rows
+    def gather_rows(
+        self,
+        layer_ptrs,
+        slots,
+        heads,
+        out_ptr: int,
+        capacity: int,
+        d: int,
+        block_size: int,
+        strides: Sequence[int],
+        elem_size: int,
+    ) -> None:
+        """Copy a step's rows of every layer and held head into a [L, H, cap, 2, d] buffer.
+
+        Same arguments as the reference's ``gather_rows`` (core/csrc/gather.cu:100-135); enqueued
+        on the current stream of ``slots``'s device, without synchronising.
+        """
+        import torch
+
+        if len(strides) != 5:
+            raise RuntimeError("gather_rows: a layout is five strides")
+        lp = _device_ptr(layer_ptrs, "gather_rows: layer_ptrs", torch.long)
+        sp = _device_ptr(slots, "gather_rows: slots", torch.long)
+        hp = _device_ptr(heads, "gather_rows: heads", torch.long)
+        st = (ctypes.c_int64 * 5)(*[int(s) for s in strides])
+        with torch.cuda.device(slots.device):
+            self._check(
+                self._lib.evs_gather_rows(
+                    lp, layer_ptrs.numel(), sp, slots.numel(), hp, heads.numel(), int(out_ptr),
+                    int(capacity), int(d), int(block_size), st, int(elem_size),
+                    _stream_of(slots.device),
+                )
+            )
+
+    def gather_blocks(
+        self,
+        layer_ptrs,
+        block_ids,
+        heads,
+        out_ptr: int,
+        capacity: int,
+        d: int,
+        block_size: int,
+        strides: Sequence[int],
+        elem_size: int,
+        slots_out=None,
+    ) -> None:
+        """:meth:`gather_rows` over whole blocks of a block table (int32 ``block_ids``).
+
+        With ``slots_out`` (int64, ``len(block_ids) * block_size``) the kernel also writes the
+        expanded slot ids, the step descriptor's tags.
+        """
+        import torch
+
+        if len(strides) != 5:
+            raise RuntimeError("gather_blocks: a layout is five strides")
+        lp = _device_ptr(layer_ptrs, "gather_blocks: layer_ptrs", torch.long)
+        bp = _device_ptr(block_ids, "gather_blocks: block_ids", torch.int32)
+        hp = _device_ptr(heads, "gather_blocks: heads", torch.long)
+        so = 0
+        if slots_out is not None:
+            so = _device_ptr(slots_out, "gather_blocks: slots_out", torch.long)
+            if slots_out.numel() < block_ids.numel() * block_size:
+                raise RuntimeError("gather_blocks: slots_out holds fewer than blocks * block_size")
+        st = (ctypes.c_int64 * 5)(*[int(s) for s in strides])
+        with torch.cuda.device(block_ids.device):
+            self._check(
+                self._lib.evs_gather_blocks(
+                    lp, layer_ptrs.numel(), bp, block_ids.numel(), hp, heads.numel(),
+                    int(out_ptr), int(capacity), int(d), int(block_size), st, int(elem_size),
+                    so or None, _stream_of(block_ids.device),
+                )
+            )
+
+    def scatter_rows(
+        self,
+        layer_ptrs,
+        slots,
+        heads,
+        in_ptr: int,
+        capacity: int,
+        d: int,
+        block_size: int,
+        strides: Sequence[int],
+        elem_size: int,
+    ) -> None:
+        """Write [L, H, cap, 2, d] rows back into the caches at ``slots`` and head slots ``heads``.
+
+        The inverse of :meth:`gather_rows`; negative slots are padding and are skipped. Replaces
+        the restore's ``PagedKV.write_rows`` (core/everserve/state/kvcopy.py:118-128).
+        """
+        import torch
+
+        if len(strides) != 5:
+            raise RuntimeError("scatter_rows: a layout is five strides")
+        lp = _device_ptr(layer_ptrs, "scatter_rows: layer_ptrs", torch.long)
+        sp = _device_ptr(slots, "scatter_rows: slots", torch.long)
+        hp = _device_ptr(heads, "scatter_rows: heads", torch.long)
+        st = (ctypes.c_int64 * 5)(*[int(s) for s in strides])
+        with torch.cuda.device(slots.device):
+            self._check(
+                self._lib.evs_scatter_rows(
+                    lp, layer_ptrs.numel(), sp, slots.numel(), hp, heads.numel(), int(in_ptr),
+                    int(capacity), int(d), int(block_size), st, int(elem_size),
+                    _stream_of(slots.device),
+                )
+            )
+
+    def copy_rows_async(self, dst_ptr: int, src_ptr: int, groups: int, bytes_: int, pitch: int,
+                        device=None) -> None:
+        """Copy ``groups`` runs of ``bytes_`` bytes spaced ``pitch`` apart on both sides, on the
+        current stream (device to host into pinned memory, or host to device)."""
+        import torch
+
+        dev = device if device is not None else torch.device("cuda", torch.cuda.current_device())
+        self._check(
+            self._lib.evs_copy_rows_async(int(dst_ptr), int(src_ptr), int(groups), int(bytes_),
+                                          int(pitch), _stream_of(dev))
+        )
+
+    # -------------------------------------------------------------- the reduction stage
+    def local_reduce(self, bufs, flags, order, out, epoch: int, timeout_ns: int, ctrl_ptr: int,
+                     state) -> None:
+        """Sum the members' bf16 buffers in ``order`` into ``out`` once their flags carry ``epoch``.
+
+        ``bufs`` int64 [MAX_ROWS] addresses, ``flags`` 64-bit [MAX_ROWS] (a tensor, or the
+        device address of host-mapped words), ``order`` int32
+        [1 + MAX_ROWS] = [count, rows...], ``state`` 64-bit [4] (zeroed once): all on the device.
+        ``ctrl_ptr`` is the device address of this member's control row (0: none). The wait ends
+        at the ABORT word or after ``timeout_ns``; the outcome is in ``state[0]``.
+        """
+        import torch
+
+        if out.dtype != torch.bfloat16 or not out.is_cuda or not out.is_contiguous():
+            raise RuntimeError("local_reduce: out must be a contiguous bf16 device tensor")
+        bp = _device_ptr(bufs, "local_reduce: bufs", torch.long)
+        if isinstance(flags, int):
+            fp = flags  # a device address, e.g. host-mapped words a host thread writes
+        else:
+            if flags.element_size() != 8 or not flags.is_cuda or flags.numel() < self.MAX_ROWS:
+                raise RuntimeError("local_reduce: flags are MAX_ROWS 64-bit words on the device")
+            fp = flags.data_ptr()
+        op = _device_ptr(order, "local_reduce: order", torch.int32)
+        if order.numel() != 1 + self.MAX_ROWS or bufs.numel() < self.MAX_ROWS:
+            raise RuntimeError("local_reduce: order is int32 [1 + MAX_ROWS], bufs [MAX_ROWS]")
+        if state.element_size() != 8 or state.numel() < 4 or not state.is_cuda:
+            raise RuntimeError("local_reduce: state is four 64-bit words on the device")
+        with torch.cuda.device(out.device):
+            self._check(
+                self._lib.evs_local_reduce(
+                    bp, fp, op, out.data_ptr(), out.numel(),
+                    int(epoch) & 0xFFFFFFFFFFFFFFFF, int(timeout_ns), int(ctrl_ptr) or None,
+                    state.data_ptr(), _stream_of(out.device),
+                )
+            )
+
+    def slot_blocks(self, maxn: int, words: int) -> int:
+        """Sequence counters for tensors up to ``maxn`` at ``words`` per thread (slot.cu:229-232)."""
+        out = ctypes.c_int64()
+        self._check(self._lib.evs_slot_blocks(int(maxn), int(words), ctypes.byref(out)))
+        return out.value
+
+    # -------------------------------------------------------------- memory
+    def host_register_mapped(self, ptr: int, bytes_: int) -> int:
+        """Pin host memory mapped into the device address space; returns the device pointer."""
+        dev = ctypes.c_void_p()
+        self._check(self._lib.evs_host_register_mapped(int(ptr), int(bytes_), ctypes.byref(dev)))
+        return int(dev.value or 0)
+
+    def host_unregister(self, ptr: int) -> None:
+        """Undo :meth:`host_register_mapped`."""
+        self._check(self._lib.evs_host_unregister(int(ptr)))
+
+    def host_alloc_mapped(self, bytes_: int) -> tuple[int, int]:
+        """Pinned coherent host memory mapped into the device: (host pointer, device pointer)."""
+        host, dev = ctypes.c_void_p(), ctypes.c_void_p()
+        self._check(
+            self._lib.evs_host_alloc_mapped(int(bytes_), ctypes.byref(host), ctypes.byref(dev))
+        )
+        return int(host.value or 0), int(dev.value or 0)
+
+    def host_free(self, ptr: int) -> None:
+        self._check(self._lib.evs_host_free(int(ptr)))
+
+    def device_alloc(self, bytes_: int) -> int:
+        """Device memory outside torch's caching allocator, zeroed."""
+        p = ctypes.c_void_p()
+        self._check(self._lib.evs_device_alloc(int(bytes_), ctypes.byref(p)))
+        return int(p.value or 0)
+
+    def device_free(self, ptr: int) -> None:
+        self._check(self._lib.evs_device_free(int(ptr)))
+
+    def memset_async(self, ptr: int, bytes_: int) -> None:
+        """Zero device memory on the current stream (a fill kernel, safe inside graph capture)."""
+        import torch
+
+        dev = torch.device("cuda", torch.cuda.current_device())
+        self._check(self._lib.evs_memset_async(int(ptr), int(bytes_), _stream_of(dev)))
+
+    def ipc_handle(self, ptr: int) -> bytes:
+        """An inter-process handle for a :meth:`device_alloc` buffer (64 bytes)."""
+        buf = (ctypes.c_uint8 * HANDLE_BYTES)()
+        self._check(self._lib.evs_ipc_handle(int(ptr), buf, HANDLE_BYTES))
+        return bytes(buf)
+
+    def ipc_open(self, handle: bytes) -> int:
+        """Map another process's buffer from its handle."""
+        if len(handle) != HANDLE_BYTES:
+            raise RuntimeError("ipc_open: not an IPC handle")
+        buf = (ctypes.c_uint8 * HANDLE_BYTES).from_buffer_copy(handle)
+        p = ctypes.c_void_p()
+        self._check(self._lib.evs_ipc_open(buf, HANDLE_BYTES, ctypes.byref(p)))
+        return int(p.value or 0)
+
+    def ipc_close(self, ptr: int) -> None:
+        self._check(self._lib.evs_ipc_close(int(ptr)))
+
+    def wall_clock_khz(self) -> int:
+        """The current device's wall-clock rate, in kHz."""
+        khz = ctypes.c_int64()
+        self._check(self._lib.evs_wall_clock_khz(ctypes.byref(khz)))
+        return khz.value
+
+
+_SOURCE: str = ""
+"""How this process got its kernels, once loaded: ``prebuilt`` or ``in-tree``."""
+
+
+@functools.lru_cache(maxsize=1)
+def load() -> Kernels:
+    """The kernels for this process: the named prebuilt, else the in-tree build.
+
+    Cached for the process, like the HIP context the library runs in.
+
+    Raises:
+        KernelsUnavailable: without a GPU, or when the build cannot be loaded here.
+    """
+    global _SOURCE
+    import torch
+
+    if not torch.cuda.is_available():
+        raise KernelsUnavailable("the Everserve MI355X kernels need a GPU")
+    named = os.environ.get(PREBUILT_ENV, "")
+    path = library_path()
+    try:
+        lib = open_library(path)
+    except OSError as e:
+        raise KernelsUnavailable(f"{path}: cannot be loaded: {e}") from e
+    _SOURCE = "prebuilt" if named else "in-tree"
+    return Kernels(lib, path)
+
+
+def source() -> str:
+    """How this process got its kernels: ``prebuilt``, ``in-tree``, or ``""`` before loading."""
+    return _SOURCE
+
+
+@functools.lru_cache(maxsize=1)
+def available() -> bool:
+    """Whether this process runs on the kernels: False without a GPU, or by choice.
+
+    ``EVERSERVE_KERNELS=torch`` takes the torch paths without loading anything. Any other reason
+    the kernels cannot load raises, so a rank never runs other paths than its peers' without an
+    operator having said so (core/everserve/kernels.py:202-221).
+
+    Raises:
+        KernelsUnavailable: a build that cannot be loaded here.
+    """
+    import torch
+
+    if os.environ.get(PATHS_ENV, "") == "torch":
+        log.info("%s=torch: the torch paths serve, the kernels are not loaded", PATHS_ENV)
+        return False
+    if not torch.cuda.is_available():
+        return False
+    load()
+    return True

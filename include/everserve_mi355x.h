@@ -1,0 +1,175 @@
+/*
+ * everserve_mi355x.h — the C ABI of libeverserve_mi355x.so, the MI355X (gfx950) per-worker KV
+ * data path: the step's KV snapshot gather, the restore scatter, and the reduction stage of the
+ * failure-detecting all-reduce.
+ *
+ * Every entry point returns 0 on success and a nonzero EVS_E* code on failure; evs_last_error()
+ * then gives a message for the calling thread. Pointers named "device" are addresses in the
+ * current HIP device's address space (HBM, or host memory mapped into it); `stream` is a
+ * hipStream_t passed as void* (NULL is the null stream). Nothing here allocates on the hot path
+ * (the gathers, the scatter and the reductions), and nothing here synchronises a stream: every
+ * kernel is enqueued on `stream` and the call returns.
+ *
+ * The reference exposes the same surface as the pybind module `everserve_kernels`
+ * (core/csrc/kernels.cpp:9-31, declared at core/csrc/kernels.h:18-59); each declaration below
+ * names the reference entry it replaces.
+ */
+#ifndef EVERSERVE_MI355X_H
+#define EVERSERVE_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Return codes. */
+#define EVS_OK 0
+#define EVS_EINVAL 1 /* a precondition failed; nothing was enqueued */
+#define EVS_EHIP 2   /* a HIP runtime call failed */
+
+/* The slot region's layout shared with the Python side (core/csrc/kernels.h:18-22: kMaxRows,
+ * kCtrlWords, kAbort, kLate, kBound). A region is MAX_ROWS control rows of CTRL_WORDS int64
+ * words; word ABORT releases a waiting reduction, word LATE receives the mask of the rows a
+ * reduction waits for past the bound, word BOUND holds that bound in nanoseconds (0 = off). */
+#define EVS_MAX_ROWS 8
+#define EVS_CTRL_WORDS 16
+#define EVS_ABORT 1
+#define EVS_LATE 11
+#define EVS_BOUND 12
+
+/* The local reduction's status word (evs_local_reduce, state[0]) once a call has finished:
+ * (epoch << 16) | (reason << 8) | late_mask. */
+#define EVS_REDUCE_DONE 0      /* every member's flag carried the call's epoch */
+#define EVS_REDUCE_ABORTED 1   /* released by the ABORT control word */
+#define EVS_REDUCE_TIMED_OUT 2 /* the hard timeout passed with members still missing */
+#define EVS_REDUCE_STATE_WORDS 4
+
+/* The message of the last failed call on this thread ("" if none). */
+const char* evs_last_error(void);
+
+/* The layout constants above as the library was built with them: out[0..4] = MAX_ROWS,
+ * CTRL_WORDS, ABORT, LATE, BOUND. The Python shim exports them as the reference module's
+ * attributes (core/csrc/kernels.cpp:12-16), which core/everserve/comm/slotkernel.py:98-120
+ * compares against its own copy. `n` must be at least 5. */
+int evs_layout_constants(int64_t* out, int64_t n);
+
+/* Copy one step's K and V rows of every layer and held head slot into a staging buffer laid out
+ * [num_layers, num_heads, capacity, 2, head_dim] (elements of elem_size bytes), on `stream`.
+ * Replaces gather_rows (core/csrc/gather.cu:100-135, kernels.h:27-29). For t < num_slots:
+ *
+ *   out[l][h][t][k][j] = layer_l[(s / block_size) * strides[0] + (s % block_size) * strides[1]
+ *                                + heads[h] * strides[2] + k * strides[3] + j * strides[4]]
+ *   with s = max(slots[t], 0)   (a negative slot id is padding and reads slot 0)
+ *
+ * strides (host array of five, in elements) are the cache layout's block, offset-in-block, head
+ * slot, K-or-V and element strides (core/everserve/state/kvcopy.py:105-116). layer_ptrs (device,
+ * num_layers int64 addresses), slots (device, int64) and heads (device, int64) are read by the
+ * kernel; rows num_slots..capacity-1 are not written. Bytes move unchanged, so fp8 (e4m3/e5m2)
+ * caches go through elem_size 1 bit-exactly. Requires elem_size in {1, 2, 4} and
+ * num_slots <= capacity; returns EVS_OK with nothing enqueued when any count is zero. The 16-byte
+ * path is taken when strides[4] == 1 and head_dim*elem_size, out and every other stride (in bytes)
+ * are multiples of 16; the caller guarantees the layer bases are 16-byte aligned then, as the
+ * reference's caller does (core/everserve/state/mirror.py:344). */
+int evs_gather_rows(const int64_t* layer_ptrs, int64_t num_layers, const int64_t* slots,
+                    int64_t num_slots, const int64_t* heads, int64_t num_heads, void* out,
+                    int64_t capacity, int64_t head_dim, int64_t block_size,
+                    const int64_t* strides, int64_t elem_size, void* stream);
+
+/* evs_gather_rows over whole blocks of a block table: the rows equal those of evs_gather_rows
+ * with slots[t] = block_ids[t / block_size] * block_size + t % block_size, t < num_blocks *
+ * block_size. When slots_out is not NULL the kernel also writes those slot ids there (device,
+ * int64, num_blocks * block_size): the step descriptor's sequence tags
+ * (proto/everserve/proto/mirror.proto:50-51). Replaces the host-side expansion of the staged
+ * block ids (core/everserve/reference/staging.py:51-94 chooses them) followed by gather_rows. */
+int evs_gather_blocks(const int64_t* layer_ptrs, int64_t num_layers, const int32_t* block_ids,
+                      int64_t num_blocks, const int64_t* heads, int64_t num_heads, void* out,
+                      int64_t capacity, int64_t head_dim, int64_t block_size,
+                      const int64_t* strides, int64_t elem_size, int64_t* slots_out,
+                      void* stream);
+
+/* The inverse of evs_gather_rows: write rows laid out [num_layers, num_heads, capacity, 2,
+ * head_dim] back into the paged caches at slots[t] and head slots heads[h]. A negative slot is
+ * padding and is skipped (nothing written). Slots must be distinct (a restore's written slot
+ * ranges are, store/src/storage.rs:430-451); with duplicates which row lands is unspecified.
+ * Replaces the restore's per-table PagedKV.write_rows scatter
+ * (core/everserve/state/mirror.py:926-937, core/everserve/state/kvcopy.py:118-128). */
+int evs_scatter_rows(const int64_t* layer_ptrs, int64_t num_layers, const int64_t* slots,
+                     int64_t num_slots, const int64_t* heads, int64_t num_heads, const void* in,
+                     int64_t capacity, int64_t head_dim, int64_t block_size,
+                     const int64_t* strides, int64_t elem_size, void* stream);
+
+/* The reduction stage of the failure-detecting all-reduce over member buffers already in this
+ * GPU's HBM (the local stage of core/csrc/slot.cu:118-224):
+ *
+ *   out[i] = bf16_rne( ((0.0f + f32(x_{o1}[i])) + f32(x_{o2}[i])) + ... )
+ *
+ * with o = order[1 .. order[0]] (device int32 [1 + EVS_MAX_ROWS], rows < EVS_MAX_ROWS),
+ * x_r = the bf16 buffer at bufs[r] (device table of EVS_MAX_ROWS int64 addresses) and bf16_rne
+ * torch's round to nearest even (NaN becomes 0x7FC0), i < n. Member r's payload is ready when
+ * flags[r] (device uint64 [EVS_MAX_ROWS]) equals `epoch`; the kernel waits for every member's flag
+ * before it reads that member. The wait is bounded: it ends when the ABORT word of `ctrl` (an
+ * EVS_CTRL_WORDS int64 row, host-mapped or device) is nonzero, or when timeout_ns has passed
+ * (timeout_ns <= 0 means 1 s); a member still missing then contributes zeros. While waiting past
+ * ctrl[EVS_BOUND] ns (0 = off), the kernel writes the mask of the rows it waits for into
+ * ctrl[EVS_LATE], and the last block that named clears it when its wait ends. `state` (device
+ * uint64 [EVS_REDUCE_STATE_WORDS], zeroed once before first use) receives in state[0], when the
+ * call finishes, (epoch << 16) | (reason << 8) | late_mask with reason one of EVS_REDUCE_*; the
+ * other words are the kernel's own and return to zero at the end of every call, so a captured
+ * HIP graph can replay it. Requires 0 <= n; out and every member buffer 2-byte aligned (16-byte
+ * aligned takes the vector path). */
+int evs_local_reduce(const int64_t* bufs, const uint64_t* flags, const int32_t* order, void* out,
+                     int64_t n, uint64_t epoch, int64_t timeout_ns, int64_t* ctrl,
+                     uint64_t* state, void* stream);
+
+/* Sequence counters the slot collective needs for tensors of up to `maxn` elements at `words`
+ * eight-byte words per thread: ceil((maxn / 2) / (256 * words)). Replaces slot_blocks
+ * (core/csrc/slot.cu:229-232). Writes the count to *out. */
+int evs_slot_blocks(int64_t maxn, int64_t words, int64_t* out);
+
+/* Pin `bytes` of host memory at `ptr`, mapped into the device address space; *device_ptr receives
+ * the address kernels use. Replaces host_register_mapped (core/csrc/gather.cu:137-144). */
+int evs_host_register_mapped(void* ptr, int64_t bytes, void** device_ptr);
+
+/* Undo evs_host_register_mapped. Replaces host_unregister (core/csrc/gather.cu:146-148). */
+int evs_host_unregister(void* ptr);
+
+/* Pinned, coherent host memory mapped into the device, allocated by the runtime (for hosts where
+ * registering existing memory is not allowed): *host_ptr and *device_ptr receive the two views.
+ * No reference counterpart; it stands in for host_register_mapped where that is refused. */
+int evs_host_alloc_mapped(int64_t bytes, void** host_ptr, void** device_ptr);
+int evs_host_free(void* host_ptr);
+
+/* Device memory outside any caching allocator, zeroed before return. Replaces device_alloc and
+ * device_free (core/csrc/slot.cu:283-290). */
+int evs_device_alloc(int64_t bytes, void** ptr);
+int evs_device_free(void* ptr);
+
+/* Zero `bytes` of device memory on `stream` with a fill kernel (a graph may capture it). Replaces
+ * memset_async (core/csrc/slot.cu:292-295). */
+int evs_memset_async(void* ptr, int64_t bytes, void* stream);
+
+/* Copy `groups` runs of `bytes` bytes, run g from src + g * pitch to dst + g * pitch, on `stream`
+ * (hipMemcpy2DAsync; one linear copy when bytes == pitch). Direction follows the pointers: the
+ * staging buffer's filled rows (num_slots of each (layer, head) run of `capacity`) to pinned host
+ * memory, or back. Stands in for the reference's zero-copy writes through a host-mapped staging
+ * file (core/everserve/state/mirror.py:349-356,614-622): the gather writes HBM at HBM speed and
+ * the copy engine moves the rows over PCIe on the side stream. */
+int evs_copy_rows_async(void* dst, const void* src, int64_t groups, int64_t bytes, int64_t pitch,
+                        void* stream);
+
+/* Inter-process memory handles (64 bytes). Replace ipc_handle, ipc_open and ipc_close
+ * (core/csrc/slot.cu:297-312). */
+int evs_ipc_handle(void* ptr, uint8_t* handle_out, int64_t handle_bytes);
+int evs_ipc_open(const uint8_t* handle, int64_t handle_bytes, void** ptr);
+int evs_ipc_close(void* ptr);
+
+/* The current device's wall-clock counter rate in kHz (the clock the bounded waits use). */
+int evs_wall_clock_khz(int64_t* khz);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EVERSERVE_MI355X_H */

@@ -1,0 +1,79 @@
+"""Seeded inputs shared by the tests: paged caches in the three layouts, raw-bit views.
+
+The literal shapes are the reference tests' (core/tests/test_gather_kernel.py:18-20,67-69,91-102):
+seven blocks of four slots, three head slots, three layers, slots [5, -1, 17, 0, 27] with one
+padding id, held heads [0, 2], capacity 8, d in {8, 6} (16-byte rows and not).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+import oracle
+
+NB, BS, H, L = 7, 4, 3, 3
+SLOTS = [5, -1, 17, 0, 27]
+HEADS = [0, 2]
+CAPACITY = 8
+LAYOUTS = ("kv_first", "blocks_first", "combined")
+DTYPES = (torch.bfloat16, torch.float16, torch.float32, torch.float8_e4m3fn)
+NP_BITS = {1: np.uint8, 2: np.uint16, 4: np.uint32}
+TORCH_BITS = {1: torch.uint8, 2: torch.int16, 4: torch.int32}
+
+
+def cache_shape(layout: str, nb: int, bs: int, h: int, d: int) -> tuple[int, ...]:
+    return {
+        "kv_first": (2, nb, bs, h, d),
+        "blocks_first": (nb, 2, bs, h, d),
+        "combined": (nb, h, bs, 2 * d),
+    }[layout]
+
+
+def caches(layout: str, d: int, dtype, n_layers: int = L, nb: int = NB, bs: int = BS, h: int = H,
+           seed: int = 3) -> list[torch.Tensor]:
+    """``n_layers`` CPU caches of N(0, 1) values (fp8: N(0, 1) / 0.05, saturated to e4m3's range)."""
+    g = torch.Generator().manual_seed(seed)
+    shape = cache_shape(layout, nb, bs, h, d)
+    out = []
+    for _ in range(n_layers):
+        x = torch.randn(shape, generator=g)
+        if dtype in (torch.float8_e4m3fn, torch.float8_e5m2):
+            x = (x / 0.05).clamp(-448, 448)
+        out.append(x.to(dtype))
+    return out
+
+
+def bits(t: torch.Tensor) -> np.ndarray:
+    """A tensor's raw bits as an unsigned numpy array (CPU)."""
+    e = t.element_size()
+    return t.detach().cpu().contiguous().view(TORCH_BITS[e]).numpy().view(NP_BITS[e])
+
+
+def strides_of(t: torch.Tensor) -> tuple[int, int, int, int, int]:
+    layout, _, _, d = oracle.recognise(t.shape)
+    return oracle.layout_strides(layout, t.stride(), d)
+
+
+def brute_gather(layers, slots, heads, capacity: int) -> np.ndarray:
+    """The gather by its definition per layout, one row at a time, with numpy indexing by
+    dimension (no strides): out[l, h, t, k, j] = the K (k=0) or V (k=1) element j of head slot
+    heads[h] at slot max(slots[t], 0)."""
+    layout, _, bs, d = oracle.recognise(layers[0].shape)
+    e = layers[0].element_size()
+    out = np.zeros((len(layers), len(heads), capacity, 2, d), dtype=NP_BITS[e])
+    for li, t in enumerate(layers):
+        a = bits(t)
+        for hi, head in enumerate(heads):
+            for ti, s in enumerate(slots):
+                s = max(int(s), 0)
+                b, o = divmod(s, bs)
+                for k in range(2):
+                    if layout == "kv_first":
+                        row = a[k, b, o, head, :]
+                    elif layout == "blocks_first":
+                        row = a[b, k, o, head, :]
+                    else:
+                        row = a[b, head, o, k * d:(k + 1) * d]
+                    out[li, hi, ti, k] = row
+    return out

@@ -1,0 +1,75 @@
+"""The C-ABI library, without a GPU: it loads, exports every entry point include/*.h declares,
+and refuses bad arguments before touching the device. No kernel is launched here."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from everserve_amd import build, kernels
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def declared() -> set[str]:
+    names = set()
+    for header in (ROOT / "include").glob("*.h"):
+        text = re.sub(r"/\*.*?\*/", "", header.read_text(), flags=re.S)
+        names |= set(re.findall(r"\b(evs_\w+)\s*\(", text))
+    return names
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return kernels.open_library(kernels.library_path())
+
+
+def test_every_declared_entry_point_is_exported_and_bound(lib):
+    names = declared()
+    assert len(names) >= 18, names
+    for name in sorted(names):
+        assert hasattr(lib, name), f"{name} is declared but not exported"
+    assert names == set(kernels.ENTRY_POINTS), names ^ set(kernels.ENTRY_POINTS)
+
+
+def test_the_region_layout_is_the_reference_modules(lib):
+    # core/csrc/kernels.h:18-22 and core/everserve/comm/slotkernel.py:55,73-80
+    words = (ctypes.c_int64 * 5)()
+    assert lib.evs_layout_constants(words, 5) == 0
+    assert list(words) == [8, 16, 1, 11, 12]
+    assert lib.evs_layout_constants(words, 4) == 1
+
+
+def test_slot_blocks_is_the_reference_formula(lib):
+    out = ctypes.c_int64()
+    for maxn, words in ((65536, 1), (65536, 16), (2, 1), (3000, 4), (0, 1)):
+        assert lib.evs_slot_blocks(maxn, words, ctypes.byref(out)) == 0
+        per_block = 256 * words
+        assert out.value == (maxn // 2 + per_block - 1) // per_block
+    assert lib.evs_slot_blocks(10, 0, ctypes.byref(out)) == 1
+
+
+def test_bad_arguments_are_refused_with_a_message(lib):
+    strides = (ctypes.c_int64 * 5)(96, 24, 8, 672, 1)
+    # an element size the kernels do not take: refused before any device call
+    rc = lib.evs_gather_rows(None, 1, None, 5, None, 2, None, 8, 8, 4, strides, 3, None)
+    assert rc == 1
+    assert b"element size" in lib.evs_last_error()
+    rc = lib.evs_gather_rows(None, 1, None, 9, None, 2, None, 8, 8, 4, strides, 2, None)
+    assert rc == 1 and b"capacity" in lib.evs_last_error()
+    rc = lib.evs_scatter_rows(None, 1, None, 5, None, 2, None, 8, 8, 4, None, 2, None)
+    assert rc == 1 and b"five strides" in lib.evs_last_error()
+    # nothing to move: success without a launch
+    assert lib.evs_gather_rows(None, 0, None, 5, None, 2, None, 8, 8, 4, strides, 2, None) == 0
+    assert lib.evs_last_error() == b""
+    rc = lib.evs_local_reduce(None, None, None, None, 4, 1, 0, None, None, None)
+    assert rc == 1 and b"null" in lib.evs_last_error()
+    rc = lib.evs_copy_rows_async(None, None, 2, 16, 8, None)
+    assert rc == 1 and b"pitch" in lib.evs_last_error()
+
+
+def test_the_build_is_stamped_with_this_trees_sources():
+    stamp = kernels._check_stamp(kernels._PACKAGE)
+    assert stamp.name == kernels.LIBRARY
+    assert build.stamp()["sources"] == kernels.stamp()["sources"]

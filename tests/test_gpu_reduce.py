@@ -1,0 +1,194 @@
+"""The HIP local reduction (the reduce stage of the failure-detecting all-reduce) on the GPU.
+
+Bits equal to the oracle's ordered fp32 sum (core/everserve/reference/arith/ops.py:63-73) at the
+reference's sizes {16384, 3000, 2} (core/tests/test_slot_kernel.py:40) and at C5 (8 buffers of
+256 x 8192); the order-sensitive inputs of core/tests/test_slot_kernel.py:50-55; and the bounded
+wait: a stalled flag ends in a timeout naming that row, the host's ABORT word releases the wait,
+the LATE word names the stalled row while the wait passes BOUND and is cleared after, and a flag
+that arrives late (host-mapped, written by the host mid-wait) completes the call normally. Every
+wait in these tests is bounded by the kernel's own timeout.
+"""
+
+import ctypes
+import threading
+import time
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from tests.cases import bits
+
+pytestmark = pytest.mark.gpu
+
+MAXW = 8
+ABORT, LATE, BOUND = 1, 11, 12
+
+
+def bf16_input(seed: int, n: int) -> torch.Tensor:
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(n, generator=g).to(torch.bfloat16)
+
+
+class Ctrl:
+    """One control row of 16 int64 words in pinned, coherent host memory mapped into the GPU."""
+
+    def __init__(self, ext):
+        self.ext = ext
+        self.host, self.dev = ext.host_alloc_mapped(16 * 8)
+        self.words = (ctypes.c_int64 * 16).from_address(self.host)
+
+    def close(self):
+        self.ext.host_free(self.host)
+
+
+class Members:
+    """k member buffers in HBM, their flags, the order, and the call's state."""
+
+    def __init__(self, inputs: dict[int, torch.Tensor], order: list[int]):
+        self.bufs_t = {r: x.cuda() for r, x in inputs.items()}
+        table = [0] * MAXW
+        for r, t in self.bufs_t.items():
+            table[r] = t.data_ptr()
+        self.bufs = torch.tensor(table, dtype=torch.long, device="cuda")
+        self.flags = torch.zeros(MAXW, dtype=torch.long, device="cuda")
+        self.order = torch.tensor([len(order), *order] + [0] * (MAXW - len(order)),
+                                  dtype=torch.int32, device="cuda")
+        self.state = torch.zeros(4, dtype=torch.long, device="cuda")
+        n = next(iter(inputs.values())).numel()
+        self.out = torch.empty(n, dtype=torch.bfloat16, device="cuda")
+
+    def publish(self, epoch: int, rows=None):
+        rows = rows if rows is not None else list(self.bufs_t)
+        f = self.flags.cpu()
+        for r in rows:
+            f[r] = epoch
+        self.flags.copy_(f)
+
+    def status(self):
+        s = int(self.state[0].item()) & 0xFFFFFFFFFFFFFFFF
+        return s >> 16, (s >> 8) & 0xFF, s & 0xFF
+
+
+@pytest.mark.parametrize("n", [16384, 3000, 2, 8 * 256 * 2 + 5])
+@pytest.mark.parametrize("order", [[0, 1, 2], [2, 0, 1], [5, 3, 7, 0, 1, 6, 2, 4]])
+def test_the_sum_is_the_ordered_fp32_sum_bit_for_bit(ext, n, order):
+    inputs = {r: bf16_input(1000 * r + n, n) for r in order}
+    m = Members(inputs, order)
+    m.publish(epoch=1)
+    ext.local_reduce(m.bufs, m.flags, m.order, m.out, 1, 10**9, 0, m.state)
+    torch.cuda.synchronize()
+    want = oracle.member_sum([bits(inputs[r]) for r in order])
+    assert np.array_equal(bits(m.out), want)
+    assert m.status() == (1, 0, 0)
+    assert m.state[1:].cpu().tolist() == [0, 0, 0]  # the kernel's counters are back at zero
+
+
+def test_the_order_of_the_sum_shows_and_is_kept(ext):
+    n = 16384
+    g = torch.Generator().manual_seed(7)
+    big = torch.randn(n, generator=g) * 2.0**20
+    small = torch.randn(n, generator=g) * 2.0**-6
+    inputs = {0: big.to(torch.bfloat16), 1: small.to(torch.bfloat16), 2: (-big).to(torch.bfloat16)}
+    in_rank = oracle.member_sum([bits(inputs[r]) for r in (0, 1, 2)])
+    in_rows = oracle.member_sum([bits(inputs[r]) for r in (0, 2, 1)])
+    assert not np.array_equal(in_rank, in_rows), "the inputs must make the order show"
+    for order, want in (([0, 1, 2], in_rank), ([0, 2, 1], in_rows)):
+        m = Members(inputs, order)
+        m.publish(epoch=9)
+        ext.local_reduce(m.bufs, m.flags, m.order, m.out, 9, 10**9, 0, m.state)
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(m.out), want)
+
+
+def test_c5_eight_buffers_of_256_by_8192(ext):
+    n = 256 * 8192
+    order = list(range(8))
+    inputs = {r: bf16_input(5 + r, n) for r in order}
+    m = Members(inputs, order)
+    m.publish(epoch=3)
+    for _ in range(3):  # replays: the state's counters reset themselves
+        ext.local_reduce(m.bufs, m.flags, m.order, m.out, 3, 10**9, 0, m.state)
+    torch.cuda.synchronize()
+    want = oracle.member_sum([bits(inputs[r]) for r in order])
+    assert np.array_equal(bits(m.out), want)
+    assert m.status() == (3, 0, 0)
+
+
+def test_a_stalled_flag_ends_in_a_timeout_that_names_it(ext):
+    n = 256 * 8192
+    order = list(range(8))
+    inputs = {r: bf16_input(5 + r, n) for r in order}
+    m = Members(inputs, order)
+    m.publish(epoch=4)
+    m.publish(epoch=3, rows=[3])  # row 3's flag stays at epoch - 1
+    t0 = time.perf_counter()
+    ext.local_reduce(m.bufs, m.flags, m.order, m.out, 4, 1_000_000, 0, m.state)  # 1 ms
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    assert m.status() == (4, 2, 1 << 3)
+    want, reason, late = oracle.reduce_protocol({r: bits(x) for r, x in inputs.items()},
+                                                {r: (3 if r == 3 else 4) for r in order}, order, 4)
+    assert (reason, late) == (2, 1 << 3)
+    assert np.array_equal(bits(m.out), want)
+    assert elapsed < 2.0, elapsed
+
+
+def test_the_abort_word_releases_the_wait(ext):
+    ctrl = Ctrl(ext)
+    try:
+        inputs = {r: bf16_input(r, 4096) for r in range(3)}
+        m = Members(inputs, [0, 1, 2])
+        m.publish(epoch=6, rows=[0, 2])  # row 1 never arrives
+        t0 = time.perf_counter()
+        ext.local_reduce(m.bufs, m.flags, m.order, m.out, 6, 5_000_000_000, ctrl.dev, m.state)
+        time.sleep(0.05)
+        ctrl.words[ABORT] = 1
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+        assert m.status() == (6, 1, 1 << 1)
+        assert elapsed < 4.0, elapsed  # well inside the 5 s timeout
+    finally:
+        ctrl.close()
+
+
+def test_the_late_word_names_the_stalled_row_then_clears(ext):
+    ctrl = Ctrl(ext)
+    try:
+        inputs = {r: bf16_input(r, 65536) for r in range(4)}
+        m = Members(inputs, [0, 1, 2, 3])
+        m.publish(epoch=2, rows=[0, 1, 3])
+        ctrl.words[BOUND] = 1_000_000  # name after 1 ms
+        seen = set()
+        ext.local_reduce(m.bufs, m.flags, m.order, m.out, 2, 300_000_000, ctrl.dev, m.state)
+        deadline = time.perf_counter() + 0.25
+        while time.perf_counter() < deadline:
+            seen.add(int(ctrl.words[LATE]))
+            time.sleep(0.001)
+        torch.cuda.synchronize()
+        assert (1 << 2) in seen, seen
+        assert seen <= {0, 1 << 2}, seen
+        assert int(ctrl.words[LATE]) == 0  # cleared by the last workgroup that named
+        assert m.status() == (2, 2, 1 << 2)
+    finally:
+        ctrl.close()
+
+
+def test_a_flag_that_arrives_late_completes_the_call(ext):
+    flags_host, flags_dev = ext.host_alloc_mapped(MAXW * 8)
+    try:
+        words = (ctypes.c_int64 * MAXW).from_address(flags_host)
+        inputs = {r: bf16_input(40 + r, 30000) for r in range(3)}
+        m = Members(inputs, [1, 0, 2])
+        for r in (0, 1):
+            words[r] = 12
+        ext.local_reduce(m.bufs, flags_dev, m.order, m.out, 12, 3_000_000_000, 0, m.state)
+        time.sleep(0.02)
+        words[2] = 12  # the last member's payload was in place all along; now its flag
+        torch.cuda.synchronize()
+        assert m.status() == (12, 0, 0)
+        want = oracle.member_sum([bits(inputs[r]) for r in (1, 0, 2)])
+        assert np.array_equal(bits(m.out), want)
+    finally:
+        ext.host_free(flags_host)
