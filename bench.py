@@ -308,8 +308,24 @@ def bench_c5(ext, steps, warmup):
         it[0] += 1
         ext.local_reduce(table, flags, order, out, 1, 10**9, 0, state)
 
-    per, _ = time_launches(reduce_once, max(steps, 4 * SETS), warmup, stream)
+    eager, _ = time_launches(reduce_once, max(steps, 4 * SETS), warmup, stream)
     torch.cuda.synchronize()
+    eager_out = [out.clone() for _, _, out in sets]
+    for _, _, out in sets:
+        out.zero_()
+    # the kernel's own cost: the 8 calls captured in a HIP graph (the reduce is capturable: no
+    # memset, its counters reset themselves) and replayed, so no host launch sits between calls
+    side = torch.cuda.Stream(device=dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        for _, table, out in sets:
+            ext.local_reduce(table, flags, order, out, 1, 10**9, 0, state)
+    replays = 25
+    per, _ = time_launches(graph.replay, replays, 3, stream)
+    per = [p / SETS for p in per]
+    torch.cuda.synchronize()
+    graph_equal = all(torch.equal(out.view(torch.int16), e.view(torch.int16))
+                      for (_, _, out), e in zip(sets, eager_out))
     ok = int(state[0].item()) == 1 << 16
     # the stalled flag: row 3 left at epoch - 1 with a 1 ms bound fires the timeout
     flags[3] = 0
@@ -323,11 +339,14 @@ def bench_c5(ext, steps, warmup):
     us = sum(per) / len(per) * 1e3
     algo = (K + 1) * N * 2
     return {
-        "config": "C5 local reduce: 8 bf16 buffers of 256 x 8192, fp32 accumulation in order",
+        "config": "C5 local reduce: 8 bf16 buffers of 256 x 8192, fp32 accumulation in order; "
+                  "8 buffer sets rotating (288 MiB, more than the Infinity Cache)",
         "us_per_call": round(us, 2),
+        "us_per_call_eager_launches": round(sum(eager) / len(eager) * 1e3, 2),
         "gbs": round(algo / us / 1e3, 1),
         "frac_of_8tbs": round(algo / us / 1e3 / PEAK_HBM_GBS, 4),
         "completed_status_ok": ok,
+        "graph_replays_equal_eager": graph_equal,
         "stalled_flag": {"timeout_ns": 1_000_000, "host_ms_to_return": round(abort_ms, 3),
                          "reason": (st >> 8) & 0xFF, "late_mask": st & 0xFF},
     }
@@ -379,34 +398,39 @@ def bench_decode_overhead(ext, steps, warmup):
     side = torch.cuda.Stream(device=dev)
     row_bytes = 2 * DH * 2
 
-    def step(snapshot: bool, i: int):
+    def step(mode: str, i: int):
         forward()
-        if snapshot:
-            done = torch.cuda.current_stream(dev).record_event()
-            side.wait_event(done)
-            with torch.cuda.stream(side):
+        if mode == "none":
+            return
+        done = torch.cuda.current_stream(dev).record_event()
+        side.wait_event(done)
+        with torch.cuda.stream(side):
+            if mode in ("both", "gather"):
                 ext.gather_rows(ptrs, slot_sets[i % 4], heads, staging.data_ptr(), B, DH, BS,
                                 strides, 2)
+            if mode in ("both", "d2h"):
                 ext.copy_rows_async(host.data_ptr(), staging.data_ptr(), Lyr * HKV,
                                     B * row_bytes, B * row_bytes, dev)
 
-    def run(snapshot: bool, k: int):
+    def run(mode: str, k: int):
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for i in range(k):
-            step(snapshot, i)
+            step(mode, i)
         torch.cuda.synchronize()
         return (time.perf_counter() - t0) / k
 
+    modes = ("none", "both", "gather", "d2h")
     for _ in range(warmup):
-        step(False, 0)
-        step(True, 0)
+        for m in modes:
+            step(m, 0)
     k = max(steps, 20)
-    offs, ons = [], []
-    for _ in range(3):  # interleaved, to share the box's drift between the two
-        offs.append(run(False, k))
-        ons.append(run(True, k))
-    off, on = min(offs), min(ons)
+    times = {m: [] for m in modes}
+    for _ in range(3):  # interleaved, so the box's drift falls on every mode alike
+        for m in modes:
+            times[m].append(run(m, k))
+    best = {m: min(v) for m, v in times.items()}
+    off, on = best["none"], best["both"]
     del w, cache
     torch.cuda.empty_cache()
     return {
@@ -417,7 +441,39 @@ def bench_decode_overhead(ext, steps, warmup):
         "step_ms_with": round(on * 1e3, 4),
         "added_us_per_step": round((on - off) * 1e6, 2),
         "added_percent": round((on - off) / off * 100, 3),
+        "added_us_gather_only": round((best["gather"] - off) * 1e6, 2),
+        "added_us_d2h_only": round((best["d2h"] - off) * 1e6, 2),
     }
+
+
+# ------------------------------------------------------------------------------ counter runs
+def pmc_workload(ext, launches=5):
+    """What the rocprofv3 counter runs measure: ``launches`` C2 gathers, then ``launches`` copies
+    of a 1 GiB bf16 tensor by an elementwise kernel (torch.neg) whose FETCH_SIZE and WRITE_SIZE
+    are known to be 1 GiB each, the scale the gather's counters are read against."""
+    import torch
+
+    L, NB, BS, H, D = 32, 8192, 16, 8, 128
+    dev = torch.device("cuda", 0)
+    layers = random_cache_layers(L, (2, NB, BS, H, D), torch.bfloat16, dev, seed=0)
+    _, slots = block_table_slots(NB, 1024, BS, seed=2)
+    n = len(slots)
+    ptrs = torch.tensor([t.data_ptr() for t in layers], dtype=torch.long, device=dev)
+    s = torch.from_numpy(slots).to(dev)
+    heads = torch.arange(H, dtype=torch.long, device=dev)
+    out = torch.empty((L, H, n, 2, D), dtype=torch.bfloat16, device=dev)
+    strides = layout_strides(layers[0])
+    for _ in range(launches):
+        ext.gather_rows(ptrs, s, heads, out.data_ptr(), n, D, BS, strides, 2)
+    torch.cuda.synchronize()
+    del layers, out
+    a = torch.randn(GIB // 2, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    b = torch.empty_like(a)
+    for _ in range(launches):
+        torch.neg(a, out=b)
+    torch.cuda.synchronize()
+    print(f"pmc workload done: {launches} gathers of {2 * L * H * n * 2 * D * 2} algorithmic "
+          f"bytes, {launches} copies of {GIB} bytes", flush=True)
 
 
 # ------------------------------------------------------------------------------ main
@@ -428,6 +484,8 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="the headline only, no other configs")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--pmc", action="store_true",
+                    help="only the counter runs' workload (5 gathers, 5 calibration copies)")
     a = ap.parse_args(argv)
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for "
@@ -440,6 +498,9 @@ def main(argv=None):
 
     ext = kernels.load()
     torch.cuda.set_device(0)
+    if a.pmc:
+        pmc_workload(ext)
+        return 0
     log(f"device {torch.cuda.get_device_name(0)}; library {ext.__file__}")
 
     c2 = bench_c2(ext, a.steps, a.warmup, blocks_too=not a.quick)

@@ -78,10 +78,12 @@ def stamp(archs: str | None = None) -> dict[str, str]:
     return {"sources": sources_digest(), "archs": archs or archs_from_env()}
 
 
-def build(out_dir: Path = PACKAGE, archs: str | None = None, verbose: bool = False) -> Path:
+def build(out_dir: Path = PACKAGE, archs: str | None = None, verbose: bool = False,
+          defines: tuple[str, ...] = ()) -> Path:
     """Compile every source for ``archs`` (``;``-separated, default gfx950) into ``out_dir``.
 
-    Always compiles: the build is the check that the sources build. Raises
+    Always compiles: the build is the check that the sources build. ``defines`` (``NAME=VALUE``)
+    override the kernels' tuning macros, for building variants side by side. Raises
     ``subprocess.CalledProcessError`` when hipcc fails.
     """
     archs = archs or archs_from_env()
@@ -94,7 +96,8 @@ def build(out_dir: Path = PACKAGE, archs: str | None = None, verbose: bool = Fal
 
     def compile_one(src: str) -> Path:
         obj = obj_dir / (Path(src).stem + ".o")
-        cmd = [cc, *HIPCC_FLAGS, *arch_flags, *includes, "-c", str(CSRC / src), "-o", str(obj)]
+        cmd = [cc, *HIPCC_FLAGS, *arch_flags, *includes, *[f"-D{d}" for d in defines], "-c",
+               str(CSRC / src), "-o", str(obj)]
         if verbose:
             print(" ".join(cmd), flush=True)
         subprocess.run(cmd, check=True, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)

@@ -6,18 +6,23 @@
 // torch's rule: core/csrc/slot.cu:118-123,203-223 and core/everserve/reference/arith/ops.py:63-73.
 // Floating-point addition is not associative, so the order is part of the result.
 //
-// Waiting is bounded. Wave 0 of every workgroup polls the flags, one lane per member, with
+// Waiting is bounded. Wave 0 of every workgroup reads the flags, one lane per row, with
 // system-scope loads (a peer's stores over xGMI, or the host's, land behind this GPU's caches),
-// and combines the lanes with a ballot. Every 32 polls it reads the wall clock and lane 0 reads
-// the ABORT control word. The wait ends when every flag has arrived, when ABORT is set, when
+// in the same round of loads as the order and the buffer table, and combines the lanes with a
+// ballot. While a member is missing it polls again; every 32 polls it reads the wall clock and
+// lane 0 reads the ABORT control word. The wait ends when every flag has arrived, when ABORT is set, when
 // another workgroup of the same call gave up, or when the hard timeout passes; a member still
 // missing then contributes zeros, as the reference's aborted reads do (slot.cu:148). Past the
 // BOUND control word (ns, 0 = off) the workgroup writes the rows it still waits for into LATE,
 // and the last workgroup that named clears LATE once its wait is over (slot.cu:29-40,174-214).
 //
 // The call's outcome is one word, state[0] = (epoch << 16) | (reason << 8) | late rows, written by
-// the last workgroup to finish. The counters behind it (state[1..3]) return to zero at the end of
-// every call, so the launch needs no memset and a captured graph can replay it.
+// the last workgroup to finish. Completion is counted in one word, state[1]: each workgroup ORs
+// its outcome into the high bits and then adds 1 to the low bits, both relaxed atomics on that
+// one location, whose single modification order puts every workgroup's outcome before the last
+// workgroup's add. No fence is needed, so no workgroup writes back or invalidates the L2 at its
+// end. state[1] and state[3] return to zero at the end of every call, so the launch needs no
+// memset and a captured graph can replay it.
 
 #include "common.hpp"
 
@@ -26,10 +31,28 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kMaxRows = EVS_MAX_ROWS;
-constexpr int kVpt = 2;            // 8-element vectors per thread per pass
-constexpr int kMaxBlocks = 1024;   // resident at once on 256 CUs: every workgroup polls once
+#ifndef EVS_REDUCE_VPT
+#define EVS_REDUCE_VPT 4
+#endif
+#ifndef EVS_REDUCE_MAX_BLOCKS
+#define EVS_REDUCE_MAX_BLOCKS 1024
+#endif
+constexpr int kVpt = EVS_REDUCE_VPT;  // 8-element vectors per thread per pass
+constexpr int kMaxBlocks = EVS_REDUCE_MAX_BLOCKS;  // all resident on 256 CUs: each polls once
 constexpr int kPollsPerCheck = 32; // flag polls between clock and ABORT reads
 constexpr int kBadOrder = 4;       // reason bit: `order` named a row outside [0, MAX_ROWS)
+constexpr int kDoneBits = 20;      // state[1]: workgroups done in bits [0, 20), outcome above
+
+// How the payload reads are ordered after the flags. 3 (default): every payload load is a buffer
+// load at agent scope (sc1), coherent on its own, so no cache is invalidated; issued after the
+// flag values returned, it sees what the producer wrote before releasing its flag. 1: one
+// acquire fence per workgroup (an L2 invalidate); 2: one per wave; 0: none, right only when every
+// payload was written before the launch.
+#ifndef EVS_REDUCE_FENCE
+#define EVS_REDUCE_FENCE 3
+#endif
+constexpr int kPayloadScope = 16;  // buffer-load cache policy: sc1, coherent at agent scope
+constexpr int kRsrcWord3 = 0x00020000;  // raw buffer resource, dword 3 (gfx9 untyped access)
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
@@ -77,65 +100,78 @@ __global__ __launch_bounds__(kThreads) void local_reduce(ReduceArgs a) {
   const int tid = threadIdx.x;
   if (tid < 64) {
     const int lane = tid;
-    int count = a.order[0];
+    // One round of independent loads: the order words, the buffer table and every row's flag
+    // (lane r holds row r's), so a call whose members are all in costs one memory latency here.
+    const int o = lane <= kMaxRows ? a.order[lane] : 0;
+    const int64_t row_addr = lane < kMaxRows ? a.bufs[lane] : 0;
+    uint64_t row_flag = lane < kMaxRows ? load_system(a.flags + lane) : 0;
+    int count = __shfl(o, 0);
     count = count < 0 ? 0 : (count > kMaxRows ? kMaxRows : count);
-    const int row = lane < count ? a.order[1 + lane] : -1;
+    // lane q < count stands for the member in order position q
+    const int listed_row = __shfl(o, (1 + lane) & 63);
     const bool listed = lane < count;
+    const int row = listed ? listed_row : -1;
     const bool valid = listed && row >= 0 && row < kMaxRows;
     uint32_t reason = __ballot(listed && !valid) ? kBadOrder : 0;
+    const int src_lane = valid ? row : 0;
 
-    const int64_t t0 = wall_clock64();
+    // every lane takes part in every shuffle: a lane left out supplies no value to read
+    int ready = __shfl(static_cast<int>(row_flag == a.epoch), src_lane);
+    uint64_t missing = __ballot(valid && !ready);
     bool named = false;
     uint32_t late_rows = 0;
-    uint64_t missing = 0;
-    for (uint64_t poll = 0;; ++poll) {
-      const bool ready = !valid || load_system(a.flags + row) == a.epoch;
-      missing = __ballot(!ready);
-      if (missing == 0) break;
-      if (poll % kPollsPerCheck == kPollsPerCheck - 1) {
-        const int64_t waited = wall_clock64() - t0;
-        uint64_t abort = 0, given_up = 0, bound_ns = 0;
-        if (lane == 0) {
-          if (a.ctrl != nullptr) {
-            abort = load_system(reinterpret_cast<const uint64_t*>(a.ctrl + EVS_ABORT));
-            bound_ns = load_system(reinterpret_cast<const uint64_t*>(a.ctrl + EVS_BOUND));
-          }
-          given_up = __hip_atomic_load(a.state + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >> 8;
-        }
-        abort = __shfl(abort, 0);
-        given_up = __shfl(given_up, 0);
-        bound_ns = __shfl(bound_ns, 0);
-        // rows this workgroup still waits for
-        const uint32_t mine = (missing >> lane) & 1 ? (1u << row) : 0u;
-        uint32_t rows = mine;
-        for (int q = 1; q < kMaxRows; q <<= 1) rows |= __shfl_xor(rows, q);
-        late_rows = rows;
-        const int64_t waited_ns = waited * 1000000 / a.clock_khz;
-        if (a.ctrl != nullptr && static_cast<int64_t>(bound_ns) > 0 &&
-            waited_ns > static_cast<int64_t>(bound_ns)) {
+    if (missing != 0) {
+      const int64_t t0 = wall_clock64();
+      for (uint64_t poll = 0;; ++poll) {
+        if (poll % kPollsPerCheck == kPollsPerCheck - 1) {
+          const int64_t waited = wall_clock64() - t0;
+          uint64_t abort = 0, given_up = 0, bound_ns = 0;
           if (lane == 0) {
-            if (!named)
-              __hip_atomic_fetch_add(a.state + 3, uint64_t{1}, __ATOMIC_RELAXED,
-                                     __HIP_MEMORY_SCOPE_AGENT);
-            // every check: another workgroup's clear may have raced this one's write
-            store_system(a.ctrl + EVS_LATE, static_cast<int64_t>(late_rows));
+            if (a.ctrl != nullptr) {
+              abort = load_system(reinterpret_cast<const uint64_t*>(a.ctrl + EVS_ABORT));
+              bound_ns = load_system(reinterpret_cast<const uint64_t*>(a.ctrl + EVS_BOUND));
+            }
+            given_up = __hip_atomic_load(a.state + 1, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT) >> (kDoneBits + 8);
           }
-          named = true;
+          abort = __shfl(abort, 0);
+          given_up = __shfl(given_up, 0);
+          bound_ns = __shfl(bound_ns, 0);
+          // rows this workgroup still waits for
+          uint32_t rows = (missing >> lane) & 1 ? (1u << row) : 0u;
+          for (int q = 1; q < kMaxRows; q <<= 1) rows |= __shfl_xor(rows, q);
+          late_rows = rows;
+          const int64_t waited_ns = waited * 1000000 / a.clock_khz;
+          if (a.ctrl != nullptr && static_cast<int64_t>(bound_ns) > 0 &&
+              waited_ns > static_cast<int64_t>(bound_ns)) {
+            if (lane == 0) {
+              if (!named)
+                __hip_atomic_fetch_add(a.state + 3, uint64_t{1}, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+              // every check: another workgroup's clear may have raced this one's write
+              store_system(a.ctrl + EVS_LATE, static_cast<int64_t>(late_rows));
+            }
+            named = true;
+          }
+          if (abort != 0) {
+            reason |= EVS_REDUCE_ABORTED;
+            break;
+          }
+          if (given_up != 0) {
+            reason |= static_cast<uint32_t>(given_up) & (EVS_REDUCE_ABORTED | EVS_REDUCE_TIMED_OUT);
+            break;
+          }
+          if (waited > a.timeout_ticks || poll >= a.max_polls) {
+            reason |= EVS_REDUCE_TIMED_OUT;
+            break;
+          }
         }
-        if (abort != 0) {
-          reason |= EVS_REDUCE_ABORTED;
-          break;
-        }
-        if (given_up != 0) {
-          reason |= static_cast<uint32_t>(given_up) & (EVS_REDUCE_ABORTED | EVS_REDUCE_TIMED_OUT);
-          break;
-        }
-        if (waited > a.timeout_ticks || poll >= a.max_polls) {
-          reason |= EVS_REDUCE_TIMED_OUT;
-          break;
-        }
+        __builtin_amdgcn_s_sleep(2);
+        row_flag = lane < kMaxRows ? load_system(a.flags + lane) : 0;
+        ready = __shfl(static_cast<int>(row_flag == a.epoch), src_lane);
+        missing = __ballot(valid && !ready);
+        if (missing == 0) break;
       }
-      __builtin_amdgcn_s_sleep(2);
     }
     if (missing == 0) late_rows = 0;
     if (named && lane == 0) {
@@ -144,7 +180,8 @@ __global__ __launch_bounds__(kThreads) void local_reduce(ReduceArgs a) {
                                  __HIP_MEMORY_SCOPE_AGENT) == 1)
         store_system(a.ctrl + EVS_LATE, 0);
     }
-    const int64_t addr = valid ? a.bufs[row] : 0;
+    const int64_t mapped_addr = __shfl(row_addr, src_lane);
+    const int64_t addr = valid ? mapped_addr : 0;
     const bool unaligned = __ballot((addr & 15) != 0) != 0;
     if (lane < kMaxRows) {
       const bool have = valid && !((missing >> lane) & 1);
@@ -155,10 +192,11 @@ __global__ __launch_bounds__(kThreads) void local_reduce(ReduceArgs a) {
       s_vectors = !unaligned;
       s_outcome = (reason << 8) | late_rows;
     }
+    // the flags were read with relaxed loads: order the payload reads after them
+    if (EVS_REDUCE_FENCE == 1) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   }
   __syncthreads();
-  // the flags were read with relaxed loads: order the payload reads after them
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  if (EVS_REDUCE_FENCE == 2) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
 
   const int count = s_count;
   const int64_t nvec = s_vectors ? a.nvec : 0;
@@ -168,17 +206,39 @@ __global__ __launch_bounds__(kThreads) void local_reduce(ReduceArgs a) {
 
   // vectors of 8 elements: one 16-byte load per member
   const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads * kVpt;
-  for (int64_t v0 = static_cast<int64_t>(blockIdx.x) * kThreads * kVpt + tid; v0 < nvec;
-       v0 += stride) {
+  for (int64_t vb = static_cast<int64_t>(blockIdx.x) * kThreads * kVpt; vb < nvec; vb += stride) {
+    const int64_t v0 = vb + tid;
     u32x4 x[kVpt][kMaxRows];
-#pragma unroll
-    for (int i = 0; i < kVpt; i++) {
-      const int64_t v = v0 + static_cast<int64_t>(i) * kThreads;
+    if (EVS_REDUCE_FENCE == 3) {
+      // a buffer resource per member over this pass's vectors: a load past the end returns 0
+      const int64_t left = (nvec - vb) * 16;
+      const int records = static_cast<int>(left < (int64_t{1} << 30) ? left : (int64_t{1} << 30));
 #pragma unroll
       for (int q = 0; q < kMaxRows; q++) {
-        x[i][q] = u32x4{0u, 0u, 0u, 0u};
-        if (v < nvec && src[q] != nullptr)
-          x[i][q] = *reinterpret_cast<const u32x4*>(src[q] + v * 8);
+        const uint64_t base = reinterpret_cast<uint64_t>(src[q] + vb * 8);
+        const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(base));
+        const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(base >> 32));
+        __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+            reinterpret_cast<void*>((static_cast<uint64_t>(hi) << 32) | lo), 0, records,
+            kRsrcWord3);
+#pragma unroll
+        for (int i = 0; i < kVpt; i++) {
+          x[i][q] = u32x4{0u, 0u, 0u, 0u};
+          if (src[q] != nullptr)
+            x[i][q] = __builtin_amdgcn_raw_buffer_load_b128(r, (i * kThreads + tid) * 16, 0,
+                                                            kPayloadScope);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < kVpt; i++) {
+        const int64_t v = v0 + static_cast<int64_t>(i) * kThreads;
+#pragma unroll
+        for (int q = 0; q < kMaxRows; q++) {
+          x[i][q] = u32x4{0u, 0u, 0u, 0u};
+          if (v < nvec && src[q] != nullptr)
+            x[i][q] = *reinterpret_cast<const u32x4*>(src[q] + v * 8);
+        }
       }
     }
 #pragma unroll
@@ -209,23 +269,30 @@ __global__ __launch_bounds__(kThreads) void local_reduce(ReduceArgs a) {
   for (int64_t e = first + static_cast<int64_t>(blockIdx.x) * kThreads + tid; e < a.n;
        e += static_cast<int64_t>(gridDim.x) * kThreads) {
     float acc = 0.0f;
-    for (int q = 0; q < count; q++) acc += src[q] != nullptr ? bf16_to_f32(src[q][e]) : 0.0f;
+    for (int q = 0; q < count; q++) {
+      uint32_t b = 0;
+      if (src[q] != nullptr)
+        b = EVS_REDUCE_FENCE == 3 ? __hip_atomic_load(reinterpret_cast<const uint16_t*>(src[q] + e),
+                                                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                  : src[q][e];
+      acc += bf16_to_f32(b);
+    }
     a.out[e] = static_cast<uint16_t>(f32_to_bf16(acc));
   }
 
   if (tid == 0) {
-    const uint32_t outcome = s_outcome;
+    const uint64_t outcome = s_outcome;
     if (outcome != 0)
-      __hip_atomic_fetch_or(a.state + 2, static_cast<uint64_t>(outcome), __ATOMIC_RELAXED,
+      __hip_atomic_fetch_or(a.state + 1, outcome << kDoneBits, __ATOMIC_RELAXED,
                             __HIP_MEMORY_SCOPE_AGENT);
-    const uint64_t done = __hip_atomic_fetch_add(a.state + 1, uint64_t{1}, __ATOMIC_ACQ_REL,
-                                                 __HIP_MEMORY_SCOPE_AGENT);
-    if (done == gridDim.x - 1) {
-      // the last workgroup: every other one's outcome is in state[2]
-      const uint64_t all = __hip_atomic_exchange(a.state + 2, uint64_t{0}, __ATOMIC_ACQ_REL,
-                                                 __HIP_MEMORY_SCOPE_AGENT);
+    const uint64_t before = __hip_atomic_fetch_add(a.state + 1, uint64_t{1}, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT);
+    if ((before & ((uint64_t{1} << kDoneBits) - 1)) == gridDim.x - 1) {
+      // the last workgroup: every other one's outcome is in the word it just added to; the
+      // next call's workgroups touch it only after this kernel has ended
+      const uint64_t all = (before >> kDoneBits) & 0xffffu;
       __hip_atomic_store(a.state + 1, uint64_t{0}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(a.state + 0, (a.epoch << 16) | (all & 0xffffu), __ATOMIC_RELEASE,
+      __hip_atomic_store(a.state + 0, (a.epoch << 16) | all, __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_SYSTEM);
     }
   }

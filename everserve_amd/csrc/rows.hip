@@ -6,25 +6,68 @@
 // K-or-V, element), so the three paged layouts and strided views share one kernel
 // (core/everserve/state/kvcopy.py:105-116; the reference kernels are core/csrc/gather.cu:29-71).
 //
-// Work is cut into tiles of (one layer, TS consecutive slots, every held head). One workgroup of
-// 256 threads owns a tile: its first TS threads turn the tile's slot ids (or block ids) into byte
-// offsets inside a layer, the first H threads the head slots, both into LDS, so each moved word
-// costs two LDS reads and no 64-bit division. Each thread then moves VPT words at a time, every
-// load in flight before the first store. A word is 16 bytes when every half-row is contiguous
-// and 16-byte aligned on both sides (bf16 d=128: 16 words a half-row, fp8 d=128: 8), else one
-// element. Within a tile words are numbered so that a wave's 64 lanes cover whole half-rows of
-// consecutive heads of one slot: in the kv_first layout that reads a block's K (or V) as one
-// contiguous stream, and writes 256-byte runs into each head's rows.
+// Work is cut into small tiles of (one layer, HG consecutive held heads, TS consecutive slots).
+// One workgroup owns a tile: its first TS threads turn the tile's slot ids (or block ids) into
+// byte offsets inside a layer, the first HG threads the head slots, both into LDS, so each moved
+// word costs two LDS reads and no 64-bit division. Each thread then moves VPT words at a time,
+// every load in flight before the first store. A word is 16 bytes when every half-row is
+// contiguous and 16-byte aligned on both sides (bf16 d=128: 16 words a half-row, fp8 d=128: 8),
+// else one element. Within a tile the words run along the staging buffer (K then V of one row,
+// row after row), so a wave stores whole rows: 1 KiB contiguous for bf16 d=128. For the gather
+// the tile numbers run through a slot range's head groups first, so the workgroups reading the
+// heads of one cache block (adjacent in every paged layout) run side by side. Tiles are kept
+// small (a few KiB) and numerous: on MI355X many short independent workgroups keep more bytes in
+// flight than fewer long ones (measured; a persistent grid with prefetched indices was slower).
 
 #include "common.hpp"
 
 namespace evs {
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kVpt = 8;             // words per thread per pass, all loads issued before stores
+// Tuning, chosen by measurement on MI355X (the defaults); the macros let a sweep build variants
+// side by side.
+#ifndef EVS_ROWS_THREADS
+#define EVS_ROWS_THREADS 128
+#endif
+#ifndef EVS_ROWS_VPT
+#define EVS_ROWS_VPT 2
+#endif
+#ifndef EVS_ROWS_NT
+#define EVS_ROWS_NT 0  // bit 0: nontemporal loads, bit 1: nontemporal stores
+#endif
+#ifndef EVS_ROWS_ORDER
+#define EVS_ROWS_ORDER 1  // 0: a wave covers consecutive heads of one slot; 1: whole staged rows
+#endif
+#ifndef EVS_ROWS_PERSIST
+#define EVS_ROWS_PERSIST 0  // > 0: a fixed grid of this many workgroups per CU looping over tiles
+#endif
+// Tile shape per direction: words a tile aims at, heads it covers (0: all), head groups fastest.
+#ifndef EVS_GATHER_TILE_WORDS
+#define EVS_GATHER_TILE_WORDS 512
+#endif
+#ifndef EVS_GATHER_HEADS_PER_TILE
+#define EVS_GATHER_HEADS_PER_TILE 2
+#endif
+#ifndef EVS_GATHER_GROUP_FASTEST
+#define EVS_GATHER_GROUP_FASTEST 1
+#endif
+#ifndef EVS_SCATTER_TILE_WORDS
+#define EVS_SCATTER_TILE_WORDS 256
+#endif
+#ifndef EVS_SCATTER_HEADS_PER_TILE
+#define EVS_SCATTER_HEADS_PER_TILE 1
+#endif
+#ifndef EVS_SCATTER_GROUP_FASTEST
+#define EVS_SCATTER_GROUP_FASTEST 0
+#endif
+
+constexpr int kThreads = EVS_ROWS_THREADS;
+constexpr int kVpt = EVS_ROWS_VPT;  // words per thread per pass, all loads issued before stores
 constexpr int kMaxTileSlots = 64;
 constexpr int kMaxHeads = 256;      // LDS table of head offsets
+constexpr int kPersist = EVS_ROWS_PERSIST;
+constexpr bool kNtLoad = (EVS_ROWS_NT & 1) != 0;
+constexpr bool kNtStore = (EVS_ROWS_NT & 2) != 0;
 
 enum Dir : int { kGather = 0, kScatter = 1 };
 enum Index : int { kBySlots = 0, kByBlocks = 1 };
@@ -46,22 +89,29 @@ struct RowsArgs {
   int64_t bs;                 // slots per block
   int bs_shift;               // log2(bs) when bs is a power of two, else -1
   int H;
+  int HG;                     // heads per tile (a tile's heads are HG consecutive of `heads`)
   int TS;                     // slots per tile
-  uint32_t tile_words;        // TS * H * 2 * W
+  int group_fastest;          // tile numbers run through head groups first
+  uint32_t tile_words;        // TS * HG * 2 * W
   FastDiv div_w;              // words per half-row
-  FastDiv div_h;              // held heads
+  FastDiv div_h;              // heads per tile
   FastDiv div_ts;             // slots per tile
-  FastDiv div_tiles;          // tiles per layer
+  FastDiv div_tiles;          // slot tiles per (layer, head group)
+  FastDiv div_groups;         // head groups
 };
 
 template <typename T>
 __device__ __forceinline__ T load_word(const char* p) {
+  if (kNtLoad) return __builtin_nontemporal_load(reinterpret_cast<const T*>(p));
   return *reinterpret_cast<const T*>(p);
 }
 
 template <typename T>
 __device__ __forceinline__ void store_word(char* p, T v) {
-  *reinterpret_cast<T*>(p) = v;
+  if (kNtStore)
+    __builtin_nontemporal_store(v, reinterpret_cast<T*>(p));
+  else
+    *reinterpret_cast<T*>(p) = v;
 }
 
 __device__ __forceinline__ int64_t block_of(int64_t s, const RowsArgs& a) {
@@ -72,38 +122,50 @@ __device__ __forceinline__ int64_t offset_in_block(int64_t s, const RowsArgs& a)
   return a.bs_shift >= 0 ? (s & (a.bs - 1)) : s % a.bs;
 }
 
-template <typename T, int D, int I>
-__global__ __launch_bounds__(kThreads) void move_rows(RowsArgs a) {
-  __shared__ int64_t s_slot[kMaxTileSlots];  // byte offset of a slot's row in a layer, -1: none
-  __shared__ int64_t s_head[kMaxHeads];      // byte offset of a head slot in a row group
+// Which (layer, head group, slot tile) a tile number names.
+struct TileId {
+  uint32_t layer, group, tile;
+};
 
-  uint32_t layer, tile;
-  a.div_tiles.divmod(blockIdx.x, layer, tile);
-  const int tid = threadIdx.x;
-  const int64_t t0 = static_cast<int64_t>(tile) * a.TS;
-
-  if (tid < a.TS) {
-    const int64_t t = t0 + tid;
-    int64_t off = -1;
-    if (t < a.n) {
-      int64_t s;
-      if (I == kByBlocks) {
-        const int64_t blk = a.blocks[a.bs_shift >= 0 ? (t >> a.bs_shift) : t / a.bs];
-        s = blk * a.bs + offset_in_block(t, a);
-        if (a.slots_out != nullptr && layer == 0) a.slots_out[t] = s;
-      } else {
-        s = a.slots[t];
-      }
-      // padding (a negative id): the gather reads slot 0, as the torch path does; the scatter
-      // writes nothing
-      if (s < 0) s = (D == kGather) ? 0 : -1;
-      if (s >= 0) off = block_of(s, a) * a.sb + offset_in_block(s, a) * a.so;
-    }
-    s_slot[tid] = off;
+__device__ __forceinline__ TileId tile_id(const RowsArgs& a, uint32_t b) {
+  TileId id;
+  uint32_t q;
+  if (a.group_fastest) {
+    // head groups fastest: the tiles that read one slot range's heads run side by side
+    a.div_groups.divmod(b, q, id.group);
+    a.div_tiles.divmod(q, id.layer, id.tile);
+  } else {
+    a.div_tiles.divmod(b, q, id.tile);
+    a.div_groups.divmod(q, id.layer, id.group);
   }
-  for (int h = tid; h < a.H; h += kThreads) s_head[h] = a.heads[h] * a.sh;
-  __syncthreads();
+  return id;
+}
 
+// Byte offset of slot t's row inside a layer, or -1 when nothing moves for it: t past the end,
+// or padding in the scatter. Padding (a negative id) makes the gather read slot 0, as the torch
+// path does (core/everserve/state/mirror.py:579). A block-table gather also writes the slot id.
+template <int D, int I>
+__device__ __forceinline__ int64_t slot_offset(const RowsArgs& a, uint32_t layer, int64_t t) {
+  if (t >= a.n) return -1;
+  int64_t s;
+  if (I == kByBlocks) {
+    const int64_t blk = a.blocks[a.bs_shift >= 0 ? (t >> a.bs_shift) : t / a.bs];
+    s = blk * a.bs + offset_in_block(t, a);
+    if (a.slots_out != nullptr && layer == 0) a.slots_out[t] = s;
+  } else {
+    s = a.slots[t];
+  }
+  if (s < 0) s = (D == kGather) ? 0 : -1;
+  return s >= 0 ? block_of(s, a) * a.sb + offset_in_block(s, a) * a.so : -1;
+}
+
+// Move one tile's words: the slots' offsets and the heads' are in LDS.
+template <typename T, int D>
+__device__ __forceinline__ void move_tile(const RowsArgs& a, const int64_t* s_slot,
+                                          const int64_t* s_head, uint32_t layer, uint32_t group,
+                                          int64_t t0) {
+  const uint32_t h0 = group * a.HG;
+  const int tid = threadIdx.x;
   const char* cache_base = reinterpret_cast<const char*>(a.layer_ptrs[layer]);
   char* cache_w = reinterpret_cast<char*>(a.layer_ptrs[layer]);
   char* rows_l = a.rows + static_cast<int64_t>(layer) * a.H * a.cap * (2 * a.half_bytes);
@@ -116,15 +178,22 @@ __global__ __launch_bounds__(kThreads) void move_rows(RowsArgs a) {
 #pragma unroll
     for (int i = 0; i < kVpt; i++) {
       const uint32_t v = v0 + i * kThreads + tid;
-      // v = ((k * TS + tl) * H + h) * W + j
       uint32_t q, j, q2, h, k, tl;
       a.div_w.divmod(v, q, j);
-      a.div_h.divmod(q, q2, h);
-      a.div_ts.divmod(q2, k, tl);
-      const int64_t slot_off = v < a.tile_words ? s_slot[tl] : -1;
+      if (EVS_ROWS_ORDER == 0) {
+        // v = ((k * TS + tl) * H + h) * W + j
+        a.div_h.divmod(q, q2, h);
+        a.div_ts.divmod(q2, k, tl);
+      } else {
+        // v = ((h * TS + tl) * 2 + k) * W + j: K then V of one staged row, row after row
+        k = q & 1u;
+        a.div_ts.divmod(q >> 1, h, tl);
+      }
+      const bool in_tile = v < a.tile_words && h0 + h < static_cast<uint32_t>(a.H);
+      const int64_t slot_off = in_tile ? s_slot[tl] : -1;
       live[i] = slot_off >= 0;
-      cache_off[i] = slot_off + s_head[live[i] ? h : 0] + k * a.skv + j * a.sj;
-      rows_off[i] = (static_cast<int64_t>(h) * a.cap + t0 + tl) * (2 * a.half_bytes) +
+      cache_off[i] = slot_off + s_head[in_tile ? h : 0] + k * a.skv + j * a.sj;
+      rows_off[i] = (static_cast<int64_t>(h0 + h) * a.cap + t0 + tl) * (2 * a.half_bytes) +
                     k * a.half_bytes + static_cast<int64_t>(j) * sizeof(T);
     }
 #pragma unroll
@@ -142,6 +211,71 @@ __global__ __launch_bounds__(kThreads) void move_rows(RowsArgs a) {
         store_word<T>(cache_w + cache_off[i], w[i]);
     }
   }
+}
+
+// One tile per workgroup.
+template <typename T, int D, int I>
+__global__ __launch_bounds__(kThreads) void move_rows(RowsArgs a) {
+  __shared__ int64_t s_slot[kMaxTileSlots];  // byte offset of a slot's row in a layer, -1: none
+  __shared__ int64_t s_head[kMaxHeads];      // byte offset of a head slot in a row group
+
+  const TileId id = tile_id(a, blockIdx.x);
+  const int tid = threadIdx.x;
+  const int64_t t0 = static_cast<int64_t>(id.tile) * a.TS;
+  if (tid < a.TS) s_slot[tid] = slot_offset<D, I>(a, id.layer, t0 + tid);
+  const int h0 = static_cast<int>(id.group) * a.HG;
+  for (int h = tid; h < a.HG && h0 + h < a.H; h += kThreads) s_head[h] = a.heads[h0 + h] * a.sh;
+  __syncthreads();
+  move_tile<T, D>(a, s_slot, s_head, id.layer, id.group, t0);
+}
+
+// A fixed grid of workgroups, each looping over tiles gridDim.x apart. The next tile's slot
+// offsets are read while the current tile's words move, into the other half of a double buffer,
+// so the index latency hides behind the data instead of preceding it.
+template <typename T, int D, int I>
+__global__ __launch_bounds__(kThreads) void move_rows_loop(RowsArgs a, uint32_t total_tiles) {
+  __shared__ int64_t s_slot[2][kMaxTileSlots];
+  __shared__ int64_t s_head[kMaxHeads];
+  const int tid = threadIdx.x;
+  // the loop keeps every head of the call in LDS (its tiles span all of them)
+  for (int h = tid; h < a.H; h += kThreads) s_head[h] = a.heads[h] * a.sh;
+  uint32_t tile = blockIdx.x;
+  if (tid < a.TS && tile < total_tiles) {
+    const TileId id = tile_id(a, tile);
+    s_slot[0][tid] = slot_offset<D, I>(a, id.layer, static_cast<int64_t>(id.tile) * a.TS + tid);
+  }
+  __syncthreads();
+  int buf = 0;
+  for (; tile < total_tiles; tile += gridDim.x) {
+    const uint32_t next = tile + gridDim.x;
+    int64_t next_off = -1;
+    if (tid < a.TS && next < total_tiles) {
+      const TileId nid = tile_id(a, next);
+      next_off = slot_offset<D, I>(a, nid.layer, static_cast<int64_t>(nid.tile) * a.TS + tid);
+    }
+    const TileId id = tile_id(a, tile);
+    move_tile<T, D>(a, s_slot[buf], s_head + id.group * a.HG, id.layer, id.group,
+                    static_cast<int64_t>(id.tile) * a.TS);
+    if (tid < a.TS) s_slot[buf ^ 1][tid] = next_off;
+    __syncthreads();
+    buf ^= 1;
+  }
+}
+
+int g_cus[64];
+
+int cu_count(int* cus) {
+  int dev = 0;
+  EVS_HIP(hipGetDevice(&dev));
+  EVS_REQUIRE(dev >= 0 && dev < 64, "device %d out of range", dev);
+  if (g_cus[dev] == 0) {
+    int n = 0;
+    EVS_HIP(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev));
+    EVS_REQUIRE(n > 0, "device %d reports no compute units", dev);
+    g_cus[dev] = n;
+  }
+  *cus = g_cus[dev];
+  return EVS_OK;
 }
 
 struct RowsCall {
@@ -164,13 +298,17 @@ struct RowsCall {
 
 template <int D, int I, typename T>
 int launch_typed(RowsArgs a, int64_t L, uint32_t W, hipStream_t stream, const char* name) {
-  const int64_t target = static_cast<int64_t>(kThreads) * kVpt;
-  const int64_t per_slot = static_cast<int64_t>(a.H) * 2 * W;
+  const int64_t target = D == kGather ? EVS_GATHER_TILE_WORDS : EVS_SCATTER_TILE_WORDS;
+  const int hpt = D == kGather ? EVS_GATHER_HEADS_PER_TILE : EVS_SCATTER_HEADS_PER_TILE;
+  a.HG = (hpt > 0 && hpt < a.H) ? hpt : a.H;
+  a.group_fastest = D == kGather ? EVS_GATHER_GROUP_FASTEST : EVS_SCATTER_GROUP_FASTEST;
+  const int64_t groups = (a.H + a.HG - 1) / a.HG;
+  const int64_t per_slot = static_cast<int64_t>(a.HG) * 2 * W;
   int64_t ts = target / per_slot;
   ts = ts < 1 ? 1 : (ts > kMaxTileSlots ? kMaxTileSlots : ts);
   if (ts > a.n) ts = a.n;
   const int64_t tiles = (a.n + ts - 1) / ts;
-  const int64_t grid = tiles * L;
+  const int64_t grid = tiles * groups * L;
   EVS_REQUIRE(ts * per_slot < (int64_t{1} << 31), "%s: a tile of %lld words is too large", name,
               static_cast<long long>(ts * per_slot));
   EVS_REQUIRE(grid < (int64_t{1} << 31), "%s: %lld workgroups exceed the launch limit", name,
@@ -178,11 +316,21 @@ int launch_typed(RowsArgs a, int64_t L, uint32_t W, hipStream_t stream, const ch
   a.TS = static_cast<int>(ts);
   a.tile_words = static_cast<uint32_t>(ts * per_slot);
   a.div_w = FastDiv(W);
-  a.div_h = FastDiv(static_cast<uint32_t>(a.H));
+  a.div_h = FastDiv(static_cast<uint32_t>(a.HG));
   a.div_ts = FastDiv(static_cast<uint32_t>(ts));
   a.div_tiles = FastDiv(static_cast<uint32_t>(tiles));
-  hipLaunchKernelGGL((move_rows<T, D, I>), dim3(static_cast<uint32_t>(grid)), dim3(kThreads), 0,
-                     stream, a);
+  a.div_groups = FastDiv(static_cast<uint32_t>(groups));
+  if (kPersist > 0) {
+    int cus = 0;
+    const int rc = cu_count(&cus);
+    if (rc != EVS_OK) return rc;
+    const int64_t blocks = grid < int64_t{cus} * kPersist ? grid : int64_t{cus} * kPersist;
+    hipLaunchKernelGGL((move_rows_loop<T, D, I>), dim3(static_cast<uint32_t>(blocks)),
+                       dim3(kThreads), 0, stream, a, static_cast<uint32_t>(grid));
+  } else {
+    hipLaunchKernelGGL((move_rows<T, D, I>), dim3(static_cast<uint32_t>(grid)), dim3(kThreads), 0,
+                       stream, a);
+  }
   EVS_LAUNCHED(name);
   return EVS_OK;
 }

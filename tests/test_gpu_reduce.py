@@ -192,3 +192,25 @@ def test_a_flag_that_arrives_late_completes_the_call(ext):
         assert np.array_equal(bits(m.out), want)
     finally:
         ext.host_free(flags_host)
+
+
+def test_a_captured_reduction_replays_like_eager_calls(ext):
+    """The reduce records no memset and resets its own counters, so a HIP graph of it replays
+    right: several replays, with eager work and synchronisations between them, each checked."""
+    n, order = 8 * 256 * 4 * 3 + 6, [3, 1, 2]
+    inputs = {r: bf16_input(70 + r, n) for r in order}
+    m = Members(inputs, order)
+    m.publish(epoch=5)
+    want = oracle.member_sum([bits(inputs[r]) for r in order])
+    side = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        ext.local_reduce(m.bufs, m.flags, m.order, m.out, 5, 10**9, 0, m.state)
+    for i in range(4):
+        m.out.fill_(i)  # eager work between the replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(m.out), want), i
+        assert m.status() == (5, 0, 0)
+        assert m.state[1:].cpu().tolist() == [0, 0, 0]

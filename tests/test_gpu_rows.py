@@ -112,3 +112,148 @@ def test_rejections_raise_not_launch(ext):
         ext.gather_rows(ptrs(layers), s.cpu(), h, out.data_ptr(), 8, 8, 4, st, 2)
     # nothing to move: returns without launching
     ext.gather_rows(ptrs(layers), s[:0], h, out.data_ptr(), 8, 8, 4, st, 2)
+
+
+def test_a_captured_gather_replays_like_an_eager_call(ext):
+    """The gather records no memset: a HIP graph of it replays right each time, eager work and
+    synchronisations between the replays, the slot ids changed in place between replays."""
+    layers = caches("kv_first", 8, torch.bfloat16, seed=21)
+    gpu = [t.cuda() for t in layers]
+    s = torch.tensor(SLOTS, dtype=torch.long, device="cuda")
+    h = torch.tensor(HEADS, dtype=torch.long, device="cuda")
+    out = torch.zeros((len(layers), len(HEADS), CAPACITY, 2, 8), dtype=torch.bfloat16, device="cuda")
+    table = ptrs(gpu)  # made before the capture: a capture records no host-to-device copy
+    strides = list(strides_of(gpu[0]))
+    side = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        ext.gather_rows(table, s, h, out.data_ptr(), CAPACITY, 8, 4, strides, 2)
+    for i, slots in enumerate([SLOTS, [27, 3, -1, 9, 0], SLOTS[::-1]]):
+        s.copy_(torch.tensor(slots))
+        out.fill_(i)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        want = oracle.gather_rows(layers, slots, HEADS, CAPACITY, 8, 4, strides_of(layers[0]), 2,
+                                  out=np.full((len(layers), len(HEADS), CAPACITY, 2, 8),
+                                              bits(torch.full((1,), float(i), dtype=torch.bfloat16))[0],
+                                              dtype=np.uint16))
+        assert np.array_equal(bits(out), want), i
+
+
+# ----------------------------------------------------------------- the configs' shapes
+def block_table(num_blocks_cache, num_blocks, bs, seed):
+    blocks = np.random.default_rng(seed).permutation(num_blocks_cache)[:num_blocks]
+    return blocks, oracle.expand_blocks(blocks, bs)
+
+
+def gpu_caches(n_layers, shape, dtype, seed):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    out = []
+    for _ in range(n_layers):
+        if dtype == torch.float8_e4m3fn:
+            out.append(torch.randn(shape, generator=g, device="cuda", dtype=torch.float16)
+                       .clamp_(-448, 448).to(dtype))
+        else:
+            out.append(torch.empty(shape, dtype=dtype, device="cuda").normal_(generator=g))
+    return out
+
+
+def test_c2_llama3_8b_gather_matches_the_oracle_on_two_layers(ext):
+    """C2's per-layer shape, two layers, every slot of the 1024 blocks checked on the CPU."""
+    L, NB, BS, H, D = 2, 8192, 16, 8, 128
+    layers = gpu_caches(L, (2, NB, BS, H, D), torch.bfloat16, seed=0)
+    _, slots = block_table(NB, 1024, BS, seed=2)
+    n = len(slots)
+    out = torch.empty((L, H, n, 2, D), dtype=torch.bfloat16, device="cuda")
+    ext.gather_rows(ptrs(layers), torch.from_numpy(slots).cuda(),
+                    torch.arange(H, dtype=torch.long, device="cuda"), out.data_ptr(), n, D, BS,
+                    list(strides_of(layers[0])), 2)
+    torch.cuda.synchronize()
+    cpu = [t.cpu() for t in layers]
+    want = oracle.gather_rows(cpu, slots, list(range(H)), n, D, BS, strides_of(cpu[0]), 2)
+    assert np.array_equal(bits(out), want)
+
+
+def test_c2_full_size_round_trip(ext):
+    """All 32 layers (16 GiB of cache): gather the 1024 blocks, scatter them into a zeroed cache,
+    and the restored blocks equal the originals on every layer; nothing else was written."""
+    L, NB, BS, H, D = 32, 8192, 16, 8, 128
+    layers = gpu_caches(L, (2, NB, BS, H, D), torch.bfloat16, seed=0)
+    blocks, slots = block_table(NB, 1024, BS, seed=2)
+    n = len(slots)
+    s = torch.from_numpy(slots).cuda()
+    heads = torch.arange(H, dtype=torch.long, device="cuda")
+    strides = list(strides_of(layers[0]))
+    out = torch.empty((L, H, n, 2, D), dtype=torch.bfloat16, device="cuda")
+    ext.gather_rows(ptrs(layers), s, heads, out.data_ptr(), n, D, BS, strides, 2)
+    fresh = [torch.zeros_like(t) for t in layers[:4]]
+    ext.scatter_rows(ptrs(fresh), s, heads, out.data_ptr(), n, D, BS, strides, 2)
+    torch.cuda.synchronize()
+    b = torch.from_numpy(blocks).cuda()
+    for orig, back in zip(layers, fresh):
+        assert torch.equal(orig[:, b].view(torch.int16), back[:, b].view(torch.int16))
+        keep = torch.ones(NB, dtype=torch.bool, device="cuda")
+        keep[b] = False
+        assert not back[:, keep].view(torch.int16).any()
+    # the other 28 layers' rows against the cache, on the device: row t of head h is block
+    # slots[t] // 16, offset slots[t] % 16 of that head
+    bi, oi = s // BS, s % BS
+    for li in range(4, L):
+        want = layers[li][:, bi, oi].permute(2, 1, 0, 3)  # [H, n, 2, D]
+        assert torch.equal(out[li].view(torch.int16), want.view(torch.int16)), li
+
+
+def test_c3_fp8_share_gather_and_copy_to_pinned_memory(ext):
+    """C3: 80 layers of a one-head fp8 e4m3 cache, 2048 blocks gathered and copied to pinned host
+    memory; the bytes equal the oracle's on a layer subset and the device staging on all."""
+    L, NB, BS, H, D = 80, 8192, 16, 1, 128
+    layers = gpu_caches(L, (2, NB, BS, H, D), torch.float8_e4m3fn, seed=3)
+    _, slots = block_table(NB, 2048, BS, seed=3)
+    n = len(slots)
+    staging = torch.empty((L, H, n, 2, D), dtype=torch.uint8, device="cuda")
+    host = torch.zeros((L, H, n, 2, D), dtype=torch.uint8, pin_memory=True)
+    ext.gather_rows(ptrs(layers), torch.from_numpy(slots).cuda(),
+                    torch.zeros(H, dtype=torch.long, device="cuda"), staging.data_ptr(), n, D, BS,
+                    list(strides_of(layers[0])), 1)
+    ext.copy_rows_async(host.data_ptr(), staging.data_ptr(), L * H, n * 2 * D, n * 2 * D)
+    torch.cuda.synchronize()
+    assert torch.equal(host, staging.cpu())
+    sub = [layers[i].cpu() for i in (0, 41, 79)]
+    want = oracle.gather_rows(sub, slots, [0], n, D, BS, strides_of(sub[0]), 1)
+    assert np.array_equal(host[[0, 41, 79]].numpy(), want)
+
+
+def test_copy_rows_moves_only_the_filled_rows(ext):
+    """A staging buffer of capacity 8 holding 5 rows per (layer, head): the 2-D copy moves the
+    5 rows of each run and leaves the host's other rows alone."""
+    L, H, cap, n, row = 3, 2, 8, 5, 32
+    dev = torch.arange(L * H * cap * row, dtype=torch.int32, device="cuda").view(torch.uint8)
+    host = torch.full((L * H * cap * row * 4,), 0xAB, dtype=torch.uint8, pin_memory=True)
+    ext.copy_rows_async(host.data_ptr(), dev.data_ptr(), L * H, n * row * 4, cap * row * 4)
+    torch.cuda.synchronize()
+    d = dev.cpu().view(L * H, cap * row * 4)
+    h = host.view(L * H, cap * row * 4)
+    assert torch.equal(h[:, : n * row * 4], d[:, : n * row * 4])
+    assert (h[:, n * row * 4:] == 0xAB).all()
+
+
+def test_c4_restore_round_trip_full_size(ext):
+    """C4: 64 seqs x 4096 tokens of Llama-3-8B rows (32 GiB) scattered into a fresh
+    16384-block cache through a seeded random-permutation block table, gathered back: equal."""
+    L, NB, BS, H, D = 32, 16384, 16, 8, 128
+    n = NB * BS
+    rows = torch.empty((L, H, n, 2, D), dtype=torch.bfloat16, device="cuda")
+    rows.normal_(generator=torch.Generator(device="cuda").manual_seed(4))
+    cache = [torch.zeros((2, NB, BS, H, D), dtype=torch.bfloat16, device="cuda") for _ in range(L)]
+    _, slots = block_table(NB, NB, BS, seed=4)
+    s = torch.from_numpy(slots).cuda()
+    heads = torch.arange(H, dtype=torch.long, device="cuda")
+    strides = list(strides_of(cache[0]))
+    ext.scatter_rows(ptrs(cache), s, heads, rows.data_ptr(), n, D, BS, strides, 2)
+    back = torch.empty((8, H, n, 2, D), dtype=torch.bfloat16, device="cuda")
+    for first in range(0, L, 8):
+        ext.gather_rows(ptrs(cache[first:first + 8]), s, heads, back.data_ptr(), n, D, BS,
+                        strides, 2)
+        torch.cuda.synchronize()
+        assert torch.equal(back.view(torch.int16), rows[first:first + 8].view(torch.int16)), first
