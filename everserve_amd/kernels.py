@@ -145,6 +145,8 @@ _SIGNATURES: tuple[tuple[str, object, tuple], ...] = (
     ),
     ("evs_scatter_rows", _I32, (_P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _P, _I64, _P)),
     ("evs_local_reduce", _I32, (_P, _P, _P, _P, _I64, ctypes.c_uint64, _I64, _P, _P, _P)),
+    ("evs_slot_all_reduce", _I32,
+     (_P, _P, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I32, _I64, _P)),
     ("evs_slot_blocks", _I32, (_I64, _I64, _P)),
     ("evs_host_register_mapped", _I32, (_P, _I64, _P)),
     ("evs_host_unregister", _I32, (_P,)),
@@ -367,6 +369,43 @@ class Kernels:
                     bp, fp, op, out.data_ptr(), out.numel(),
                     int(epoch) & 0xFFFFFFFFFFFFFFFF, int(timeout_ns), int(ctrl_ptr) or None,
                     state.data_ptr(), _stream_of(out.device),
+                )
+            )
+
+    slot_timeout_ns = 30 * 10**9
+    """How long a slot_all_reduce waits for a member before it stops by itself, ABORT aside."""
+
+    def slot_all_reduce(self, inp, out, bufs, ctrl_ptr: int, order, seqs, row: int, maxn: int,
+                        words: int, push: bool) -> None:
+        """The slot collective: sum bf16 ``inp`` over the row's members, graph-capturable.
+
+        The reference's arguments (core/csrc/slot.cu:234-281): ``bufs`` int64 [MAX_ROWS] device
+        table of word buffers, ``ctrl_ptr`` the device address of the region's control rows,
+        ``order`` int32 [1 + MAX_ROWS], ``seqs`` int64 counters, ``row`` this member's row.
+        """
+        import torch
+
+        if inp.dtype != torch.bfloat16 or out.dtype != torch.bfloat16:
+            raise RuntimeError("slot_all_reduce: bf16 only")
+        if not (inp.is_cuda and out.is_cuda and bufs.is_cuda and seqs.is_cuda and order.is_cuda):
+            raise RuntimeError("slot_all_reduce: tensors must be on the device")
+        if not (inp.is_contiguous() and out.is_contiguous()):
+            raise RuntimeError("slot_all_reduce: contiguous only")
+        if out.numel() != inp.numel():
+            raise RuntimeError("slot_all_reduce: out and inp differ in size")
+        if order.dtype != torch.int32 or order.numel() != 1 + self.MAX_ROWS:
+            raise RuntimeError(f"slot_all_reduce: the order is int32 [count, rows...] of "
+                               f"{1 + self.MAX_ROWS}")
+        bp = _device_ptr(bufs, "slot_all_reduce: bufs", torch.long)
+        if seqs.dtype != torch.long or not seqs.is_contiguous():
+            raise RuntimeError("slot_all_reduce: seqs are contiguous int64")
+        with torch.cuda.device(inp.device):
+            self._check(
+                self._lib.evs_slot_all_reduce(
+                    inp.data_ptr(), out.data_ptr(), inp.numel(), bp, int(ctrl_ptr),
+                    order.data_ptr(), seqs.data_ptr(), seqs.numel(), int(row), int(maxn),
+                    int(words), 1 if push else 0, int(self.slot_timeout_ns),
+                    _stream_of(inp.device),
                 )
             )
 

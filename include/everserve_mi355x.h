@@ -123,6 +123,25 @@ int evs_local_reduce(const int64_t* bufs, const uint64_t* flags, const int32_t* 
                      int64_t n, uint64_t epoch, int64_t timeout_ns, int64_t* ctrl,
                      uint64_t* state, void* stream);
 
+/* The slot collective: sum bf16 `inp` (n elements, even, n <= maxn) over the members `order`
+ * lists, in that order, into `out`, on `stream`. Replaces slot_all_reduce (core/csrc/slot.cu:
+ * 234-281, kernels.h:43-45) argument for argument, plus num_seqs and timeout_ns:
+ *   bufs      device table of EVS_MAX_ROWS addresses, each row's word buffer: [2][maxn/2]
+ *             uint64 words (pull) or [2][EVS_MAX_ROWS][maxn/2] (push);
+ *   ctrl      device address of the region's control rows (EVS_MAX_ROWS x EVS_CTRL_WORDS int64);
+ *             row `row`'s ABORT and BOUND are read, its LATE written;
+ *   order     device int32 [1 + EVS_MAX_ROWS] = [count, rows...];
+ *   seqs      device int64 [num_seqs], num_seqs > evs_slot_blocks(maxn, 1): a sequence counter
+ *             per workgroup, then the count of workgroups that named a late member; zeroed at a
+ *             membership change (core/everserve/comm/slotkernel.py:713-727);
+ *   words     8-byte words per thread: 1, 2, 4, 8 or 16; push nonzero for the push variant.
+ * A word is (sequence << 32) | two bf16. The wait ends when every member's words carry the
+ * call's sequence number, at the ABORT word, or after timeout_ns (<= 0: 30 s; the reference waits
+ * for ABORT alone); a member's missing words then sum as zeros. */
+int evs_slot_all_reduce(const void* inp, void* out, int64_t n, const int64_t* bufs, int64_t* ctrl,
+                        const int32_t* order, int64_t* seqs, int64_t num_seqs, int64_t row,
+                        int64_t maxn, int64_t words, int push, int64_t timeout_ns, void* stream);
+
 /* Sequence counters the slot collective needs for tensors of up to `maxn` elements at `words`
  * eight-byte words per thread: ceil((maxn / 2) / (256 * words)). Replaces slot_blocks
  * (core/csrc/slot.cu:229-232). Writes the count to *out. */
