@@ -283,6 +283,85 @@ def bench_c4(ext, steps, warmup):
     }
 
 
+# ------------------------------------------------------------------------------ restore host path
+def bench_restore_host(ext, steps, warmup):
+    """The restore from the store's table files: this build's Restorer against the reference's
+    procedure (core/everserve/state/mirror.py:916-939: map, index_select into pinned memory,
+    copy to the device, write_rows), on the same C4-shaped tables in /dev/shm."""
+    import shutil
+    import tempfile
+
+    import numpy as np
+    import torch
+
+    from everserve_amd.state.kvcopy import PagedKV
+    from everserve_amd.state.restore import Restorer, Table
+
+    L, NB, BS, H, D = 4, 16384, 16, 8, 128
+    n = NB * BS
+    row_bytes = 2 * D * 2
+    dev = torch.device("cuda", 0)
+    shm = "/dev/shm" if os.path.isdir("/dev/shm") else None
+    tmp = tempfile.mkdtemp(prefix="evs-restore-", dir=shm)
+    try:
+        base = np.random.default_rng(4).integers(0, 1 << 16, size=n * 2 * D, dtype=np.uint16)
+        base &= 0xBFFF  # finite bf16 values (clears the top exponent bit: no inf or NaN)
+        paths = {}
+        for layer in range(L):
+            for h in range(H):
+                table = layer * 1000 + h
+                paths[table] = os.path.join(tmp, f"table{table}.rows")
+                base.tofile(paths[table])
+        written = [(0, n)]
+        caches = [torch.zeros((2, NB, BS, H, D), dtype=torch.bfloat16, device=dev) for _ in range(L)]
+        head_map = {h: (h + 3) % H for h in range(H)}
+        restorer = Restorer(ext, caches)
+        tables = [Table.open(t, p, written) for t, p in paths.items()]
+        restorer.restore(tables[:2], head_map)  # warm: page in, pinned buffers touched
+        t0 = time.perf_counter()
+        rows = restorer.restore(tables, head_map)
+        ours_s = time.perf_counter() - t0
+        payload = rows * row_bytes
+        # check: layer 2's new head slot of theirs 5, slot ids 0..15
+        got = caches[2][:, 0, :, head_map[5]].permute(1, 0, 2).contiguous()  # [16, 2, D]
+        want = torch.from_numpy(base[: 16 * 2 * D].view(np.int16).reshape(16, 2, D).copy())
+        ok = bool(torch.equal(got.view(torch.int16).cpu(), want))
+
+        # the reference's procedure on the same files (torch's gather on one host thread)
+        paged = PagedKV.of(caches[0])
+        idx = torch.cat([torch.arange(s, s + c, dtype=torch.long) for s, c in written])
+        idx_dev = idx.to(dev)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for table, path in paths.items():
+            layer, head = divmod(table, 1000)
+            src = torch.from_file(path, shared=True, size=n * 2 * D, dtype=torch.bfloat16)
+            src = src.view(n, 2, D)
+            pinned = torch.empty((idx.numel(), 2, D), dtype=torch.bfloat16, pin_memory=True)
+            torch.index_select(src, 0, idx, out=pinned)
+            on_device = pinned.to(dev, non_blocking=True)
+            paged.write_rows(caches[layer], idx_dev, head_map[head], on_device.transpose(0, 1))
+        torch.cuda.synchronize()
+        ref_s = time.perf_counter() - t0
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+    del caches
+    torch.cuda.empty_cache()
+    return {
+        "config": f"restore of {L * H} store tables of C4 shape ([262144, 2, 128] bf16, 128 MiB "
+                  f"each, every slot written) from /dev/shm files into a fresh 16384-block cache "
+                  f"at other head slots",
+        "payload_bytes": payload,
+        "ours_s": round(ours_s, 3),
+        "ours_gbs": round(payload / ours_s / 1e9, 2),
+        "reference_procedure_s": round(ref_s, 3),
+        "reference_procedure_gbs": round(payload / ref_s / 1e9, 2),
+        "speedup": round(ref_s / ours_s, 2),
+        "rows_check": ok,
+        "host_threads": restorer._threads,
+    }
+
+
 # ------------------------------------------------------------------------------ C5 reduce
 def bench_c5(ext, steps, warmup):
     import torch
@@ -548,6 +627,7 @@ def main(argv=None):
             "rows_equal_gather_rows": c2["blocks_equal"]}
     if not a.quick:
         for name, fn in (("c3_fp8_gather_d2h", bench_c3), ("c4_restore", bench_c4),
+                         ("restore_host_path", bench_restore_host),
                          ("c5_reduce", bench_c5), ("decode_overhead", bench_decode_overhead)):
             log(f"{name} ...")
             result["extra"][name] = fn(ext, a.steps, a.warmup)

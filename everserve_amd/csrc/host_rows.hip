@@ -1,0 +1,78 @@
+// The restore's host side: copy a table's written slot ranges into one contiguous run of rows,
+// on several host threads (the reference does it on one, with torch.index_select,
+// core/everserve/state/mirror.py:926-932). The source is a store table mapped from shared memory,
+// [num_slots, row_bytes]; the destination is pinned memory the next H2D copy reads.
+
+#include <algorithm>
+#include <cstring>
+#include <thread>
+#include <vector>
+
+#include "common.hpp"
+
+namespace evs {
+namespace {
+
+constexpr int64_t kMinBytesPerThread = int64_t{4} << 20;  // below this a thread costs more than it copies
+
+// Copy output rows [r0, r1) of the concatenated ranges.
+void copy_rows(const char* src, int64_t row_bytes, const int64_t* starts, const int64_t* counts,
+               const int64_t* first_row, int64_t nranges, char* dst, int64_t r0, int64_t r1) {
+  // the range that holds output row r0
+  int64_t lo = 0, hi = nranges - 1;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi + 1) / 2;
+    if (first_row[mid] <= r0) lo = mid; else hi = mid - 1;
+  }
+  int64_t r = r0;
+  for (int64_t k = lo; k < nranges && r < r1; k++) {
+    const int64_t in_range = r - first_row[k];
+    const int64_t take = std::min(counts[k] - in_range, r1 - r);
+    if (take <= 0) continue;
+    std::memcpy(dst + r * row_bytes, src + (starts[k] + in_range) * row_bytes,
+                static_cast<size_t>(take * row_bytes));
+    r += take;
+  }
+}
+
+}  // namespace
+}  // namespace evs
+
+extern "C" int evs_host_gather_ranges(const void* src, int64_t row_bytes, const int64_t* starts,
+                                      const int64_t* counts, int64_t nranges, void* dst,
+                                      int64_t max_threads, int64_t* rows_out) {
+  evs::clear_error();
+  EVS_REQUIRE(row_bytes > 0 && nranges >= 0 && max_threads >= 1,
+              "evs_host_gather_ranges: row_bytes > 0, nranges >= 0, max_threads >= 1");
+  EVS_REQUIRE(nranges == 0 || (src != nullptr && dst != nullptr && starts != nullptr &&
+                               counts != nullptr),
+              "evs_host_gather_ranges: null pointer");
+  std::vector<int64_t> first_row(static_cast<size_t>(nranges) + 1, 0);
+  for (int64_t k = 0; k < nranges; k++) {
+    EVS_REQUIRE(starts[k] >= 0 && counts[k] >= 0, "evs_host_gather_ranges: negative range %lld",
+                static_cast<long long>(k));
+    first_row[k + 1] = first_row[k] + counts[k];
+  }
+  const int64_t rows = first_row[nranges];
+  if (rows_out != nullptr) *rows_out = rows;
+  if (rows == 0) return EVS_OK;
+  const int64_t bytes = rows * row_bytes;
+  int64_t threads = bytes / evs::kMinBytesPerThread;
+  threads = threads < 1 ? 1 : (threads > max_threads ? max_threads : threads);
+  const char* s = static_cast<const char*>(src);
+  char* d = static_cast<char*>(dst);
+  if (threads == 1) {
+    evs::copy_rows(s, row_bytes, starts, counts, first_row.data(), nranges, d, 0, rows);
+    return EVS_OK;
+  }
+  std::vector<std::thread> pool;
+  pool.reserve(static_cast<size_t>(threads));
+  for (int64_t t = 0; t < threads; t++) {
+    const int64_t r0 = rows * t / threads;
+    const int64_t r1 = rows * (t + 1) / threads;
+    pool.emplace_back(evs::copy_rows, s, row_bytes, starts, counts, first_row.data(), nranges, d,
+                      r0, r1);
+  }
+  for (auto& th : pool) th.join();
+  return EVS_OK;
+}

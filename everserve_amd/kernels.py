@@ -156,6 +156,7 @@ _SIGNATURES: tuple[tuple[str, object, tuple], ...] = (
     ("evs_device_free", _I32, (_P,)),
     ("evs_memset_async", _I32, (_P, _I64, _P)),
     ("evs_copy_rows_async", _I32, (_P, _P, _I64, _I64, _I64, _P)),
+    ("evs_host_gather_ranges", _I32, (_P, _I64, _P, _P, _I64, _P, _I64, _P)),
     ("evs_ipc_handle", _I32, (_P, _P, _I64)),
     ("evs_ipc_open", _I32, (_P, _I64, _P)),
     ("evs_ipc_close", _I32, (_P,)),
@@ -335,6 +336,26 @@ class Kernels:
             self._lib.evs_copy_rows_async(int(dst_ptr), int(src_ptr), int(groups), int(bytes_),
                                           int(pitch), _stream_of(dev))
         )
+
+    def host_gather_ranges(self, src_ptr: int, row_bytes: int, starts, counts, dst_ptr: int,
+                           max_threads: int = 16) -> int:
+        """Copy the rows of slot ranges of a host table into ``dst_ptr`` on host threads.
+
+        ``starts`` and ``counts`` are int64 numpy arrays; returns the rows copied.
+        """
+        import numpy as np
+
+        st = np.ascontiguousarray(starts, dtype=np.int64)
+        ct = np.ascontiguousarray(counts, dtype=np.int64)
+        if st.shape != ct.shape:
+            raise RuntimeError("host_gather_ranges: starts and counts differ in length")
+        rows = ctypes.c_int64()
+        self._check(
+            self._lib.evs_host_gather_ranges(int(src_ptr), int(row_bytes), st.ctypes.data,
+                                             ct.ctypes.data, st.size, int(dst_ptr),
+                                             int(max_threads), ctypes.byref(rows))
+        )
+        return rows.value
 
     # -------------------------------------------------------------- the reduction stage
     def local_reduce(self, bufs, flags, order, out, epoch: int, timeout_ns: int, ctrl_ptr: int,

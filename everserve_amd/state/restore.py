@@ -1,0 +1,152 @@
+"""The restore's copy into this rank's cache: a lost rank's store tables to the paged cache.
+
+The reference's loop (core/everserve/state/mirror.py:916-939) takes each table the store names,
+maps it from shared memory as ``[num_slots, 2, d]``, gathers the written rows on the host with
+``torch.index_select`` into pinned memory, copies them to the device and scatters them with
+``PagedKV.write_rows`` into the head slot the rank assigned. Published at 2.1-2.6 GB/s
+(bench/runs/2026-10-05-shm-commit-4gpu/RESULT.md:36,45-46): the host gather bounds it.
+
+:class:`Restorer` does the same table by table, in chunks, and keeps three things busy at once:
+host threads gathering chunk i+1's rows into one pinned buffer (``evs_host_gather_ranges``), the
+copy engine moving chunk i from the other pinned buffer to the device (``evs_copy_rows_async``),
+and the scatter kernel writing chunk i into the cache (``evs_scatter_rows``). Rows land byte for
+byte where ``write_rows`` puts them.
+"""
+
+from __future__ import annotations
+
+import os
+import time
+from dataclasses import dataclass
+from typing import Iterable, Mapping, Sequence
+
+import numpy as np
+import torch
+
+from everserve_amd.state.kvcopy import PagedKV
+
+HEAD_STRIDE = 1_000
+"""A table id is layer * 1000 + head slot (core/everserve/state/mirror.py:59)."""
+
+
+@dataclass
+class Table:
+    """One store table of the lost rank: its rows and the slots written in it.
+
+    ``rows`` is the table's bytes, ``[num_slots, row_bytes]`` (a numpy array, typically a
+    read-only memory map of the table file); ``written`` the ``(start, count)`` slot ranges the
+    store names (proto/everserve/proto/mirror.proto:102-117).
+    """
+
+    table: int
+    rows: np.ndarray
+    written: Sequence[tuple[int, int]]
+
+    @property
+    def layer(self) -> int:
+        return self.table // HEAD_STRIDE
+
+    @property
+    def head(self) -> int:
+        return self.table % HEAD_STRIDE
+
+    @classmethod
+    def open(cls, table: int, path: str, written: Sequence[tuple[int, int]]) -> "Table":
+        """The table file at ``path`` mapped read-only."""
+        return cls(table, np.memmap(path, dtype=np.uint8, mode="r"), written)
+
+
+class Restorer:
+    """Writes restored tables into ``layers`` (this rank's caches, in layer order)."""
+
+    def __init__(self, ext, layers: Sequence[torch.Tensor], chunk_bytes: int = 64 << 20,
+                 threads: int | None = None) -> None:
+        first = layers[0]
+        self._ext = ext
+        self.layers = list(layers)
+        self.paged = PagedKV.of(first)
+        self.device = first.device
+        self._ptrs = torch.tensor([t.data_ptr() for t in layers], dtype=torch.long,
+                                  device=self.device)
+        self._strides = list(self.paged.layout_strides(first))
+        self._elem = first.element_size()
+        self._row_bytes = 2 * self.paged.head_dim * self._elem
+        self._chunk_rows = max(1, chunk_bytes // self._row_bytes)
+        self._threads = threads or min(16, len(os.sched_getaffinity(0)))
+        n, rb = self._chunk_rows, self._row_bytes
+        self._host = [torch.empty(n * rb, dtype=torch.uint8, pin_memory=True) for _ in range(2)]
+        self._host_slots = [torch.empty(n, dtype=torch.long, pin_memory=True) for _ in range(2)]
+        self._dev = [torch.empty(n * rb, dtype=torch.uint8, device=self.device) for _ in range(2)]
+        self._dev_slots = [torch.empty(n, dtype=torch.long, device=self.device) for _ in range(2)]
+        self._heads: dict[int, torch.Tensor] = {}
+        self._done: list[torch.cuda.Event | None] = [None, None]
+        self.timing: dict[str, float] = {}
+
+    def _head(self, h: int) -> torch.Tensor:
+        if h not in self._heads:
+            self._heads[h] = torch.tensor([h], dtype=torch.long, device=self.device)
+        return self._heads[h]
+
+    def restore(self, tables: Iterable[Table], head_map: Mapping[int, int]) -> int:
+        """Write every table whose head slot ``head_map`` names into its new head slot.
+
+        Returns the rows written, over every table. Synchronises the device at the end, as the
+        reference's restore does (core/everserve/state/mirror.py:938-939).
+        """
+        t0 = time.perf_counter()
+        stream = torch.cuda.current_stream(self.device)
+        rb, n_chunk = self._row_bytes, self._chunk_rows
+        total = 0
+        buf = 0
+        for table in tables:
+            if table.head not in head_map or not table.written:
+                continue
+            if table.rows.nbytes % rb:
+                raise ValueError(f"table {table.table}: {table.rows.nbytes} bytes is not a whole "
+                                 f"number of {rb}-byte rows")
+            starts = np.array([s for s, _ in table.written], dtype=np.int64)
+            counts = np.array([c for _, c in table.written], dtype=np.int64)
+            if (starts < 0).any() or (counts < 0).any() or \
+                    (starts + counts).max() * rb > table.rows.nbytes:
+                raise ValueError(f"table {table.table}: a written range lies outside the table")
+            first_row = np.concatenate([[0], np.cumsum(counts)])
+            rows = int(first_row[-1])
+            src = table.rows.ctypes.data
+            layer_ptr = self._ptrs[table.layer:table.layer + 1]
+            head = self._head(head_map[table.head])
+            for c0 in range(0, rows, n_chunk):
+                c1 = min(rows, c0 + n_chunk)
+                # the ranges, trimmed to output rows [c0, c1)
+                k0 = int(np.searchsorted(first_row, c0, side="right")) - 1
+                k1 = int(np.searchsorted(first_row, c1, side="left"))
+                st = starts[k0:k1].copy()
+                ct = counts[k0:k1].copy()
+                skip = c0 - first_row[k0]
+                st[0] += skip
+                ct[0] -= skip
+                ct[-1] -= first_row[k1] - c1 if k1 <= len(counts) else 0
+                done = self._done[buf]
+                if done is not None:
+                    done.synchronize()  # the copy out of this pinned buffer has finished
+                got = self._ext.host_gather_ranges(src, rb, st, ct, self._host[buf].data_ptr(),
+                                                   self._threads)
+                assert got == c1 - c0
+                slots = self._host_slots[buf].numpy()
+                at = 0
+                for s, c in zip(st.tolist(), ct.tolist()):
+                    slots[at:at + c] = np.arange(s, s + c, dtype=np.int64)
+                    at += c
+                n = c1 - c0
+                self._ext.copy_rows_async(self._dev[buf].data_ptr(), self._host[buf].data_ptr(),
+                                          1, n * rb, n * rb, self.device)
+                self._dev_slots[buf][:n].copy_(self._host_slots[buf][:n], non_blocking=True)
+                self._ext.scatter_rows(layer_ptr, self._dev_slots[buf][:n], head,
+                                       self._dev[buf].data_ptr(), n, self.paged.head_dim,
+                                       self.paged.block_size, self._strides, self._elem)
+                self._done[buf] = stream.record_event()
+                total += n
+                buf ^= 1
+        torch.cuda.synchronize(self.device)
+        self.timing = {"copy_s": time.perf_counter() - t0, "rows": total,
+                       "bytes": total * rb}
+        return total

@@ -178,6 +178,16 @@ int evs_memset_async(void* ptr, int64_t bytes, void* stream);
 int evs_copy_rows_async(void* dst, const void* src, int64_t groups, int64_t bytes, int64_t pitch,
                         void* stream);
 
+/* The restore's host gather: copy the rows of `nranges` slot ranges (starts[k], counts[k]) of a
+ * store table at `src` ([num_slots, row_bytes], a shared-memory mapping) into `dst`, one range
+ * after another, on up to max_threads host threads; *rows_out (if not NULL) receives the row
+ * count. Host memory only, no device call. Replaces the per-table torch.index_select of the
+ * restore (core/everserve/state/mirror.py:926-932); the ranges are the table's written
+ * SlotRanges (proto/everserve/proto/mirror.proto:102-117). */
+int evs_host_gather_ranges(const void* src, int64_t row_bytes, const int64_t* starts,
+                           const int64_t* counts, int64_t nranges, void* dst, int64_t max_threads,
+                           int64_t* rows_out);
+
 /* Inter-process memory handles (64 bytes). Replace ipc_handle, ipc_open and ipc_close
  * (core/csrc/slot.cu:297-312). */
 int evs_ipc_handle(void* ptr, uint8_t* handle_out, int64_t handle_bytes);

@@ -1,0 +1,75 @@
+"""The restore path end to end on the GPU: a rank's caches gathered into staging rows, committed
+into the store's tables (the store's own commit, restated in the oracle), then restored into
+another rank's caches at other head slots by everserve_amd.state.restore.Restorer, chunk by chunk.
+
+Checked byte for byte: every written slot's rows in the new head slot equal the source rows, the
+other head slots are untouched (core/tests/test_kvcopy.py:162-189 states the same round trip for
+the torch path).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from everserve_amd.state.restore import Restorer, Table
+from tests.cases import bits, caches, strides_of
+
+pytestmark = pytest.mark.gpu
+
+
+def commit(src, slots, held, cap, steps=1):
+    """The store's tables after committing `slots` of every layer and held head of `src`."""
+    _, nb, bs, d = oracle.recognise(src[0].shape)
+    e = src[0].element_size()
+    staged = oracle.gather_rows(src, slots, held, cap, d, bs, strides_of(src[0]), e)
+    step = oracle.staged_step("s", list(range(len(src))), held, cap, d, e, slots,
+                              "bfloat16" if e == 2 else "uint8")
+    tables, written = {}, {}
+    oracle.store_commit(staged.view(np.uint8).reshape(-1), step, tables, nb * bs, written, steps)
+    return tables, written
+
+
+@pytest.mark.parametrize("layout", ["kv_first", "blocks_first", "combined"])
+@pytest.mark.parametrize("chunk_bytes", [64, 1 << 20])
+def test_restored_rows_land_in_the_new_head_slots(ext, layout, chunk_bytes):
+    nb, bs, h, d = 40, 4, 3, 8
+    src = caches(layout, d, torch.bfloat16, n_layers=3, nb=nb, bs=bs, h=h, seed=31)
+    slots = [5, -1, 17, 0, 27, 26, 25, 3, 100, 101, 102, 159, 50]
+    held = [0, 2]
+    tables, written = commit(src, slots, held, cap=16)
+    moves = {0: 1, 2: 0}  # the unit in their head slot 0 goes to our 1, theirs 2 to our 0
+    dst = [torch.zeros_like(t).cuda() for t in src]
+    r = Restorer(ext, dst, chunk_bytes=chunk_bytes, threads=4)
+    rows = r.restore([Table(t, rows, oracle.written_ranges(written[t])) for t, rows in tables.items()],
+                     moves)
+    live = sorted({s for s in slots if s >= 0})
+    assert rows == len(live) * len(src) * len(held)
+    want = oracle.gather_rows(src, live, held, len(live), d, bs, strides_of(src[0]), 2)
+    cpu = [t.cpu() for t in dst]
+    got = oracle.gather_rows(cpu, live, [moves[x] for x in held], len(live), d, bs,
+                             strides_of(cpu[0]), 2)
+    assert np.array_equal(got, want)
+    # head slot 2 of ours was never a target: still zero
+    untouched = oracle.gather_rows(cpu, list(range(nb * bs)), [2], nb * bs, d, bs,
+                                   strides_of(cpu[0]), 2)
+    assert not untouched.any()
+
+
+def test_an_incremental_restore_copies_only_the_later_slots(ext):
+    src = caches("kv_first", 8, torch.bfloat16, n_layers=2, nb=16, bs=4, h=2, seed=41)
+    tables, written = {}, {}
+    _, _, bs, d = oracle.recognise(src[0].shape)
+    for step, slots in ((1, [0, 1, 2, 3]), (2, [9, 10])):
+        staged = oracle.gather_rows(src, slots, [0, 1], 8, d, bs, strides_of(src[0]), 2)
+        desc = oracle.staged_step("s", [0, 1], [0, 1], 8, d, 2, slots, "bfloat16")
+        oracle.store_commit(staged.view(np.uint8).reshape(-1), desc, tables, 64, written, step)
+    dst = [torch.zeros_like(t).cuda() for t in src]
+    Restorer(ext, dst).restore(
+        [Table(t, rows, oracle.written_ranges(written[t], since_step=1)) for t, rows in tables.items()],
+        {0: 0, 1: 1})
+    cpu = [t.cpu() for t in dst]
+    assert np.array_equal(
+        oracle.gather_rows(cpu, [9, 10], [0, 1], 2, d, bs, strides_of(cpu[0]), 2),
+        oracle.gather_rows(src, [9, 10], [0, 1], 2, d, bs, strides_of(src[0]), 2))
+    assert not oracle.gather_rows(cpu, [0, 1, 2, 3], [0, 1], 4, d, bs, strides_of(cpu[0]), 2).any()

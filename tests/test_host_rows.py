@@ -1,0 +1,51 @@
+"""The restore's host gather (evs_host_gather_ranges), on the CPU: it is host code only.
+
+Against numpy's concatenation of the same row ranges, for one range, many small ones, empty ones,
+sizes that take one thread and sizes that take several, and bad ranges refused.
+"""
+
+import numpy as np
+import pytest
+
+from everserve_amd import kernels
+
+
+@pytest.fixture(scope="module")
+def ext():
+    path = kernels.library_path()
+    return kernels.Kernels(kernels.open_library(path), path)
+
+
+def concat(table, row_bytes, starts, counts):
+    rows = table.reshape(-1, row_bytes)
+    parts = [rows[s:s + c] for s, c in zip(starts, counts)]
+    return np.concatenate(parts).reshape(-1) if parts else np.zeros(0, np.uint8)
+
+
+@pytest.mark.parametrize("num_slots,row_bytes,ranges", [
+    (64, 16, [(3, 1), (9, 1), (12, 1)]),                 # the store test's written slots
+    (4096, 512, [(0, 4096)]),                             # every slot
+    (4096, 512, [(5, 0), (7, 3), (100, 0), (200, 50)]),  # empty ranges among others
+    (70000, 512, [(i * 7, 3) for i in range(9000)]),     # many short ranges, several threads
+    (100000, 256, [(0, 40000), (50000, 50000)]),          # large, several threads
+])
+def test_the_rows_of_the_ranges_in_order(ext, num_slots, row_bytes, ranges):
+    rng = np.random.default_rng(num_slots)
+    table = rng.integers(0, 255, size=num_slots * row_bytes, dtype=np.uint8)
+    starts = np.array([s for s, _ in ranges], dtype=np.int64)
+    counts = np.array([c for _, c in ranges], dtype=np.int64)
+    want = concat(table, row_bytes, starts, counts)
+    dst = np.full(max(1, want.size), 0xEE, dtype=np.uint8)
+    rows = ext.host_gather_ranges(table.ctypes.data, row_bytes, starts, counts, dst.ctypes.data, 8)
+    assert rows == counts.sum()
+    assert np.array_equal(dst[:want.size], want)
+
+
+def test_bad_ranges_are_refused(ext):
+    table = np.zeros(64, np.uint8)
+    dst = np.zeros(64, np.uint8)
+    with pytest.raises(kernels.KernelError, match="negative range"):
+        ext.host_gather_ranges(table.ctypes.data, 16, np.array([-1]), np.array([1]),
+                               dst.ctypes.data)
+    with pytest.raises(kernels.KernelError, match="row_bytes"):
+        ext.host_gather_ranges(table.ctypes.data, 0, np.array([0]), np.array([1]), dst.ctypes.data)
