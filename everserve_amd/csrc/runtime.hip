@@ -173,6 +173,43 @@ extern "C" int evs_copy_rows_async(void* dst, const void* src, int64_t groups, i
   return EVS_OK;
 }
 
+extern "C" int evs_event_create(int system_fence, void** event) {
+  evs::clear_error();
+  EVS_REQUIRE(event != nullptr, "evs_event_create: null output");
+  hipEvent_t e = nullptr;
+  const unsigned flags =
+      hipEventDisableTiming | (system_fence ? 0u : static_cast<unsigned>(hipEventDisableSystemFence));
+  EVS_HIP(hipEventCreateWithFlags(&e, flags));
+  *event = e;
+  return EVS_OK;
+}
+
+extern "C" int evs_event_destroy(void* event) {
+  evs::clear_error();
+  EVS_HIP(hipEventDestroy(static_cast<hipEvent_t>(event)));
+  return EVS_OK;
+}
+
+extern "C" int evs_event_record(void* event, void* stream) {
+  evs::clear_error();
+  EVS_HIP(hipEventRecord(static_cast<hipEvent_t>(event), evs::as_stream(stream)));
+  return EVS_OK;
+}
+
+extern "C" int evs_event_synchronize(void* event) {
+  evs::clear_error();
+  EVS_HIP(hipEventSynchronize(static_cast<hipEvent_t>(event)));
+  return EVS_OK;
+}
+
+extern "C" int evs_stream_handoff(void* producing, void* waiting, void* event) {
+  evs::clear_error();
+  EVS_REQUIRE(event != nullptr, "evs_stream_handoff: null event");
+  EVS_HIP(hipEventRecord(static_cast<hipEvent_t>(event), evs::as_stream(producing)));
+  EVS_HIP(hipStreamWaitEvent(evs::as_stream(waiting), static_cast<hipEvent_t>(event), 0));
+  return EVS_OK;
+}
+
 extern "C" int evs_ipc_handle(void* ptr, uint8_t* handle_out, int64_t handle_bytes) {
   evs::clear_error();
   EVS_REQUIRE(handle_out != nullptr && handle_bytes == sizeof(hipIpcMemHandle_t),

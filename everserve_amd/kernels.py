@@ -157,6 +157,11 @@ _SIGNATURES: tuple[tuple[str, object, tuple], ...] = (
     ("evs_memset_async", _I32, (_P, _I64, _P)),
     ("evs_copy_rows_async", _I32, (_P, _P, _I64, _I64, _I64, _P)),
     ("evs_host_gather_ranges", _I32, (_P, _I64, _P, _P, _I64, _P, _I64, _P)),
+    ("evs_event_create", _I32, (_I32, _P)),
+    ("evs_event_destroy", _I32, (_P,)),
+    ("evs_event_record", _I32, (_P, _P)),
+    ("evs_event_synchronize", _I32, (_P,)),
+    ("evs_stream_handoff", _I32, (_P, _P, _P)),
     ("evs_ipc_handle", _I32, (_P, _P, _I64)),
     ("evs_ipc_open", _I32, (_P, _I64, _P)),
     ("evs_ipc_close", _I32, (_P,)),
@@ -473,6 +478,27 @@ class Kernels:
 
         dev = torch.device("cuda", torch.cuda.current_device())
         self._check(self._lib.evs_memset_async(int(ptr), int(bytes_), _stream_of(dev)))
+
+    # -------------------------------------------------------------- stream ordering
+    def event_create(self, system_fence: bool = False) -> int:
+        """A HIP event with timing off; without the system-scope fence unless asked for."""
+        ev = ctypes.c_void_p()
+        self._check(self._lib.evs_event_create(1 if system_fence else 0, ctypes.byref(ev)))
+        return int(ev.value or 0)
+
+    def event_destroy(self, event: int) -> None:
+        self._check(self._lib.evs_event_destroy(int(event)))
+
+    def event_record(self, event: int, stream) -> None:
+        self._check(self._lib.evs_event_record(int(event), int(stream.cuda_stream)))
+
+    def event_synchronize(self, event: int) -> None:
+        self._check(self._lib.evs_event_synchronize(int(event)))
+
+    def stream_handoff(self, producing, waiting, event: int) -> None:
+        """``waiting`` runs its later work after everything ``producing`` enqueued so far."""
+        self._check(self._lib.evs_stream_handoff(int(producing.cuda_stream),
+                                                 int(waiting.cuda_stream), int(event)))
 
     def ipc_handle(self, ptr: int) -> bytes:
         """An inter-process handle for a :meth:`device_alloc` buffer (64 bytes)."""

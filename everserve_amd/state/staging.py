@@ -1,0 +1,430 @@
+"""The per-step snapshot: a step's committed rows, every layer and held head, to pinned host memory.
+
+The reference's step path is ``MirrorCommittedKV.save`` / ``commit`` / ``_gather_step`` /
+``_staging`` / ``_describe`` (core/everserve/state/mirror.py:536-800) over ``_GatherKernel``
+(mirror.py:311-370). There, layers are marked as the forward runs. ``commit`` orders a side
+stream after the forward with an event and launches one ``gather_rows`` that writes the rows
+straight into a host-mapped staging file over PCIe. A sender thread waits for the side stream
+and sends the step's ``StagedStep`` descriptor to the store.
+
+:class:`StepStager` keeps that interface and the descriptor, and moves the data differently:
+
+* **The gather runs on the producing stream**, right behind the forward's last write, into a
+  staging buffer in HBM (``evs_gather_rows``, one launch for every layer). At decode sizes it
+  is a few microseconds of HBM time.
+* **A fence-less event** (``evs_event_create(0)``) is recorded behind it. This costs the step
+  thread a few microseconds and the device nothing.
+* **A copy thread** waits for that event on the host. Only then does it issue the copy of the
+  step's rows to pinned host memory (``evs_copy_rows_async``) on its own stream. That copy
+  uses the DMA engine while the next forward runs. When it has landed, the thread calls the
+  caller's ``sink`` with the step's descriptor and the host bytes.
+
+Why no stream waits on another: on MI355X, a stream that waits on a pending event from another
+stream (``hipStreamWaitEvent``) slowed the Llama-3-8B-shaped decode step it followed by about
+260 us. That held with or without the event's system-scope fence. An already-completed event
+costs about nothing to wait on. Here no device queue ever waits on another.
+
+Staging buffers are pooled as in the reference (mirror.py:588-642). Capacities are
+``max(8, next_pow2(n))``, and at most ``depth + 1`` buffer pairs are kept. A buffer returns to
+the pool only after its sink has returned, so a gather never overwrites rows still being copied.
+"""
+
+from __future__ import annotations
+
+import queue
+import threading
+import time
+from dataclasses import dataclass, field
+from typing import Callable, Mapping, Sequence
+
+import numpy as np
+import torch
+
+from everserve_amd.state.kvcopy import HeadSlot, PagedKV, layer_index
+
+HEAD_STRIDE = 1_000
+"""Table id = layer * 1000 + head slot (core/everserve/state/mirror.py:59)."""
+
+DTYPE_NAMES = {
+    torch.bfloat16: "bfloat16",
+    torch.float16: "float16",
+    torch.float32: "float32",
+    torch.float8_e4m3fn: "float8_e4m3fn",
+    torch.float8_e5m2: "float8_e5m2",
+    torch.int8: "int8",
+    torch.uint8: "uint8",
+}
+"""The dtype names the store knows (core/everserve/state/mirror.py:49-58)."""
+
+
+class StagingError(Exception):
+    """A staged step failed on the copy thread; raised on the step thread at the next call."""
+
+
+def capacity_for(n: int) -> int:
+    """Rows a staging buffer holds for a step of ``n`` slots (core/everserve/state/mirror.py:596)."""
+    if n < 1:
+        raise ValueError(f"a step stages at least one slot, got {n}")
+    return max(8, 1 << (n - 1).bit_length())
+
+
+def describe(stage: str, layers: Sequence[int], heads: Sequence[HeadSlot], capacity: int,
+             head_dim: int, elem: int, slots: Sequence[int], dtype: str) -> dict:
+    """The ``StagedStep`` descriptor of rows staged as ``[L, H, capacity, 2, d]``.
+
+    Field for field core/everserve/state/mirror.py:778-800 (proto/everserve/proto/mirror.proto:
+    32-54). Row t of (layer ``l``, head index ``h``) is at ``l * layer_stride + h * head_stride +
+    t * row_bytes``. Negative slot ids are padding, which the store skips.
+    """
+    row_bytes = 2 * head_dim * elem
+    return {
+        "stage": stage,
+        "base_offset": 0,
+        "layer_stride": len(heads) * capacity * row_bytes,
+        "head_stride": capacity * row_bytes,
+        "layers": sorted(int(x) for x in layers),
+        "heads": [int(h) for h in heads],
+        "table_stride": HEAD_STRIDE,
+        "slots": [int(s) for s in slots],
+        "dtype": dtype,
+        "shape": [2, head_dim],
+    }
+
+
+class GatherKernel:
+    """A step's gather as launches of ``gather_rows``, for the caches of one rank.
+
+    Same role as the reference's ``_GatherKernel`` (core/everserve/state/mirror.py:311-370). It
+    holds the layers' base addresses on the device and each layer's five strides. When every
+    layer shares one shape, stride and dtype (the normal case), a step of every layer is one
+    launch. Otherwise each layer is its own launch with its own strides, still the same kernel:
+    the reference's torch path per layer has no counterpart here.
+    """
+
+    def __init__(self, ext, layers: Sequence[torch.Tensor], paged: PagedKV) -> None:
+        first = layers[0]
+        if any(t.dtype != first.dtype for t in layers):
+            raise ValueError("every layer's cache must have one dtype")
+        if any(t.device != first.device for t in layers):
+            raise ValueError("every layer's cache must be on one device")
+        self._ext = ext
+        self.paged = paged
+        self.device = first.device
+        self._ptrs = torch.tensor([t.data_ptr() for t in layers], dtype=torch.long,
+                                  device=first.device)
+        self._strides = [tuple(PagedKV.of(t).layout_strides(t)) for t in layers]
+        for t in layers:
+            p = PagedKV.of(t)
+            if p.block_size != paged.block_size or p.head_dim != paged.head_dim:
+                raise ValueError("every layer's cache must have one block size and head size")
+        self.uniform = all(s == self._strides[0] for s in self._strides)
+        self.elem = first.element_size()
+        self.num_layers = len(layers)
+
+    def gather(self, slots: torch.Tensor, heads: torch.Tensor, out_ptr: int, capacity: int,
+               layers: Sequence[int] | None = None) -> None:
+        """Write rows ``[0, n)`` of every listed layer (all by default) into ``[L, H, capacity, 2, d]``
+        at ``out_ptr``, on the current stream."""
+        d, bs = self.paged.head_dim, self.paged.block_size
+        every = layers is None or len(layers) == self.num_layers
+        if every and self.uniform:
+            self._ext.gather_rows(self._ptrs, slots, heads, out_ptr, capacity, d, bs,
+                                  self._strides[0], self.elem)
+            return
+        layer_bytes = heads.numel() * capacity * 2 * d * self.elem
+        for layer in (range(self.num_layers) if layers is None else sorted(layers)):
+            self._ext.gather_rows(self._ptrs[layer:layer + 1], slots, heads,
+                                  out_ptr + layer * layer_bytes, capacity, d, bs,
+                                  self._strides[layer], self.elem)
+
+
+@dataclass
+class Stage:
+    """One pooled staging pair: ``[L, H, capacity, 2, d]`` rows in HBM and in pinned host memory."""
+
+    name: str
+    capacity: int
+    num_heads: int
+    device_rows: torch.Tensor
+    host_rows: torch.Tensor
+    device_slots: torch.Tensor
+    host_slots: torch.Tensor
+
+    def host_bytes(self) -> np.ndarray:
+        """The pinned rows as bytes (a view, no copy)."""
+        return self.host_rows.numpy()
+
+
+@dataclass
+class StepGather:
+    """One step's rows on their way to the host (core/everserve/state/mirror.py:374-387)."""
+
+    n: int
+    heads: tuple[HeadSlot, ...]
+    stage: Stage
+    filled: set[int] = field(default_factory=set)
+
+
+@dataclass
+class StagedJob:
+    """A committed step: what the sink receives once its rows are in pinned host memory."""
+
+    epoch: int
+    step: int
+    counts: dict
+    gather: StepGather | None
+    gathered: int = 0
+    """The fence-less event behind the step's gather (0 for a step with no rows)."""
+    descriptor: dict | None = None
+    stage_bytes: np.ndarray | None = None
+    done: threading.Event = field(default_factory=threading.Event)
+    error: BaseException | None = None
+    times: dict = field(default_factory=dict)
+
+
+class StepStager:
+    """The rank's step path: ``save`` per layer, ``commit`` per step, ``sink`` per staged step.
+
+    ``kv_caches`` maps layer names to the rank's cache tensors; they are ordered by the layer
+    index in their names, as the reference's ``register`` orders them (mirror.py:517-520).
+    ``heads`` are the held head slots. ``sink(job)`` runs on the copy thread with
+    ``job.descriptor`` and ``job.stage_bytes`` valid. When it returns, the staging pair goes
+    back to the pool. ``depth`` bounds the steps in flight: a commit with ``depth`` steps
+    outstanding waits for the oldest, as the reference's does (mirror.py:664-669).
+    """
+
+    def __init__(self, ext, kv_caches: Mapping[str, torch.Tensor], heads: Sequence[HeadSlot],
+                 sink: Callable[[StagedJob], None], depth: int = 2,
+                 stage_prefix: str = "stage") -> None:
+        if depth < 1:
+            raise ValueError(f"depth must be at least 1, got {depth}")
+        ordered = sorted((layer_index(n), n, t) for n, t in kv_caches.items())
+        self.layers = [(n, t) for _, n, t in ordered]
+        self._layer_of = {n: i for i, (n, _) in enumerate(self.layers)}
+        first = self.layers[0][1]
+        if not first.is_cuda:
+            raise ValueError("the step path stages device caches")
+        self.paged = PagedKV.of(first)
+        self.device = first.device
+        self.dtype = first.dtype
+        if self.dtype not in DTYPE_NAMES:
+            raise ValueError(f"no store dtype name for {self.dtype}")
+        self.heads = tuple(sorted(int(h) for h in heads))
+        self._ext = ext
+        self._kernel = GatherKernel(ext, [t for _, t in self.layers], self.paged)
+        self._heads_dev = torch.tensor(self.heads, dtype=torch.long, device=self.device)
+        self._sink = sink
+        self._depth = depth
+        self._prefix = stage_prefix
+        self._stage_seq = 0
+        self._pool: list[Stage] = []
+        self._pool_lock = threading.Lock()
+        self._events: list[int] = []
+        self._events_lock = threading.Lock()
+        self._step: StepGather | None = None
+        self._in_flight: dict[int, StagedJob] = {}
+        self._in_flight_lock = threading.Lock()
+        self._failed: BaseException | None = None
+        self.stats = {"steps": 0, "step_thread_s": 0.0, "backpressure_waits": 0,
+                      "backpressure_s": 0.0, "bytes_staged": 0, "copy_s": 0.0}
+        """``step_thread_s`` is what commits cost the step thread, ``backpressure_s`` included."""
+        self._copy_stream = torch.cuda.Stream(device=self.device)
+        self._ready = ext.event_create(True)  # the host reads what this one orders
+        self._queue: queue.Queue[StagedJob | None] = queue.Queue()
+        self._thread = threading.Thread(target=self._copy_loop, daemon=True,
+                                        name="everserve-stage-copy")
+        self._thread.start()
+
+    # ---------------------------------------------------------------- the step thread
+    def save(self, layer_name: str, kv_layer: torch.Tensor, slots: torch.Tensor) -> None:
+        """Mark this layer's rows at ``slots`` for the step's gather (mirror.py:536-566).
+
+        Reads no device memory on the calling thread. ``slots`` may hold negative padding ids:
+        the kernel reads row 0 for them and the store skips them.
+        """
+        self._check_failed()
+        layer = self._layer_of[layer_name]
+        if self.layers[layer][1].data_ptr() != kv_layer.data_ptr():
+            raise ValueError(f"layer {layer_name} is not the cache tensor the stager was given")
+        g = self._step
+        if g is None:
+            g = self._step = self._begin(slots)
+        elif g.n != slots.shape[0]:
+            raise ValueError(f"one slot mapping per step: layer {layer_name} has "
+                             f"{slots.shape[0]} slots, the step has {g.n}")
+        g.filled.add(layer)
+
+    def _begin(self, slots: torch.Tensor) -> StepGather:
+        n = int(slots.shape[0])
+        stage = self._staging(n)
+        # the step's own copy of its slot ids, ordered on the producing stream, so a later
+        # change to the caller's tensor cannot reach the gather or the descriptor
+        stage.device_slots[:n].copy_(slots.reshape(-1), non_blocking=True)
+        return StepGather(n, self.heads, stage)
+
+    def commit(self, epoch: int, step: int, committed_tokens: Mapping) -> None:
+        """Gather the step's marked layers behind the forward and queue the copy; never waits
+        for the device (mirror.py:644-680)."""
+        self._check_failed()
+        t0 = time.perf_counter()
+        g, self._step = self._step, None
+        job = StagedJob(epoch, step, dict(committed_tokens), g)
+        job.times["commit"] = t0
+        if g is not None and g.filled:
+            cur = torch.cuda.current_stream(self.device)
+            self._kernel.gather(g.stage.device_slots[:g.n], self._heads_dev,
+                                g.stage.device_rows.data_ptr(), g.stage.capacity,
+                                sorted(g.filled))
+            job.gathered = self._event()
+            self._ext.event_record(job.gathered, cur)
+        with self._in_flight_lock:
+            oldest = min(self._in_flight) if len(self._in_flight) >= self._depth else None
+        if oldest is not None:
+            self.stats["backpressure_waits"] += 1
+            tw = time.perf_counter()
+            self.fence(oldest)
+            self.stats["backpressure_s"] += time.perf_counter() - tw
+        with self._in_flight_lock:
+            self._in_flight[step] = job
+        self._queue.put(job)
+        self.stats["steps"] += 1
+        self.stats["step_thread_s"] += time.perf_counter() - t0
+
+    def fence(self, step: int) -> None:
+        """Wait until the sink has taken ``step``; raise if staging it failed."""
+        with self._in_flight_lock:
+            job = self._in_flight.get(step)
+        if job is None:
+            return
+        job.done.wait()
+        with self._in_flight_lock:
+            self._in_flight.pop(step, None)
+        if job.error is not None:
+            raise StagingError(f"staging step {step} failed: {job.error}") from job.error
+
+    def flush(self) -> None:
+        """Wait for every committed step."""
+        with self._in_flight_lock:
+            steps = sorted(self._in_flight)
+        for s in steps:
+            self.fence(s)
+
+    def close(self) -> None:
+        """Finish the steps in flight, stop the copy thread and free the staging memory."""
+        if self._thread.is_alive():
+            self._queue.put(None)
+            self._thread.join()
+        with self._pool_lock:
+            self._pool.clear()
+        with self._events_lock:
+            events, self._events = self._events, []
+        for e in events + [self._ready]:
+            self._ext.event_destroy(e)
+        self._ready = 0
+
+    def __enter__(self) -> "StepStager":
+        return self
+
+    def __exit__(self, *exc) -> None:
+        self.close()
+
+    def _check_failed(self) -> None:
+        if self._failed is not None:
+            raise StagingError(f"the copy thread failed: {self._failed}") from self._failed
+
+    # ---------------------------------------------------------------- staging pairs
+    def _staging(self, n: int) -> Stage:
+        """A staging pair with capacity ``max(8, next_pow2(n))``, from the pool when one fits."""
+        capacity = capacity_for(n)
+        with self._pool_lock:
+            for i, st in enumerate(self._pool):
+                if st.capacity == capacity and st.num_heads == len(self.heads):
+                    return self._pool.pop(i)
+        self._stage_seq += 1
+        shape = (len(self.layers), len(self.heads), capacity, 2, self.paged.head_dim)
+        nbytes = int(np.prod(shape)) * self._kernel.elem
+        return Stage(
+            name=f"{self._prefix}{self._stage_seq}.rows",
+            capacity=capacity,
+            num_heads=len(self.heads),
+            device_rows=torch.empty(nbytes, dtype=torch.uint8, device=self.device),
+            host_rows=torch.empty(nbytes, dtype=torch.uint8, pin_memory=True),
+            device_slots=torch.empty(capacity, dtype=torch.long, device=self.device),
+            host_slots=torch.empty(capacity, dtype=torch.long, pin_memory=True),
+        )
+
+    def _release(self, stage: Stage) -> None:
+        """Return a pair to the pool, keeping at most ``depth + 1`` (mirror.py:636-642)."""
+        with self._pool_lock:
+            if len(self._pool) <= self._depth:
+                self._pool.append(stage)
+
+    def _event(self) -> int:
+        with self._events_lock:
+            if self._events:
+                return self._events.pop()
+        return self._ext.event_create(False)
+
+    def _recycle(self, event: int) -> None:
+        with self._events_lock:
+            self._events.append(event)
+
+    # ---------------------------------------------------------------- the copy thread
+    def _copy_loop(self) -> None:
+        while True:
+            job = self._queue.get()
+            if job is None:
+                return
+            try:
+                self._stage_job(job)
+            except Exception as e:  # noqa: BLE001 - surfaced on the step thread
+                job.error = e
+                if self._failed is None:
+                    self._failed = e
+            finally:
+                job.done.set()
+
+    def _stage_job(self, job: StagedJob) -> None:
+        g = job.gather
+        if g is None or not g.filled:
+            if g is not None:
+                self._release(g.stage)
+            job.times["ready"] = time.perf_counter()
+            self._sink(job)
+            return
+        try:
+            self._ext.event_synchronize(job.gathered)  # a host wait: no device queue waits
+            job.times["gathered"] = t0 = time.perf_counter()
+            st, n = g.stage, g.n
+            row_bytes = 2 * self.paged.head_dim * self._kernel.elem
+            heads = len(g.heads)
+            with torch.cuda.stream(self._copy_stream):
+                if len(g.filled) == len(self.layers):
+                    self._ext.copy_rows_async(st.host_rows.data_ptr(), st.device_rows.data_ptr(),
+                                              len(self.layers) * heads, n * row_bytes,
+                                              st.capacity * row_bytes, self.device)
+                else:
+                    layer_bytes = heads * st.capacity * row_bytes
+                    for layer in sorted(g.filled):
+                        at = layer * layer_bytes
+                        self._ext.copy_rows_async(st.host_rows.data_ptr() + at,
+                                                  st.device_rows.data_ptr() + at, heads,
+                                                  n * row_bytes, st.capacity * row_bytes,
+                                                  self.device)
+                self._ext.copy_rows_async(st.host_slots.data_ptr(), st.device_slots.data_ptr(),
+                                          1, n * 8, n * 8, self.device)
+                self._ext.event_record(self._ready, self._copy_stream)
+            self._ext.event_synchronize(self._ready)
+            job.times["ready"] = t1 = time.perf_counter()
+            self.stats["copy_s"] += t1 - t0
+            self.stats["bytes_staged"] += len(g.filled) * heads * n * row_bytes
+            job.descriptor = describe(st.name, sorted(g.filled), g.heads, st.capacity,
+                                      self.paged.head_dim, self._kernel.elem,
+                                      st.host_slots[:n].tolist(), DTYPE_NAMES[self.dtype])
+            job.stage_bytes = st.host_bytes()
+            self._sink(job)
+            job.times["sent"] = time.perf_counter()
+        finally:
+            job.stage_bytes = None
+            self._recycle(job.gathered)
+            self._release(g.stage)
