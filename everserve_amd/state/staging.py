@@ -137,6 +137,21 @@ class GatherKernel:
                                   out_ptr + layer * layer_bytes, capacity, d, bs,
                                   self._strides[layer], self.elem)
 
+    def gather_blocks(self, block_ids: torch.Tensor, heads: torch.Tensor, out_ptr: int,
+                      capacity: int, slots_out: torch.Tensor) -> None:
+        """Write every slot of ``block_ids`` (int32), block by block, for every layer into
+        ``[L, H, capacity, 2, d]`` at ``out_ptr``, and the slot ids into ``slots_out``."""
+        d, bs = self.paged.head_dim, self.paged.block_size
+        if self.uniform:
+            self._ext.gather_blocks(self._ptrs, block_ids, heads, out_ptr, capacity, d, bs,
+                                    self._strides[0], self.elem, slots_out=slots_out)
+            return
+        layer_bytes = heads.numel() * capacity * 2 * d * self.elem
+        for layer in range(self.num_layers):
+            self._ext.gather_blocks(self._ptrs[layer:layer + 1], block_ids, heads,
+                                    out_ptr + layer * layer_bytes, capacity, d, bs,
+                                    self._strides[layer], self.elem, slots_out=slots_out)
+
 
 @dataclass
 class Stage:
@@ -149,6 +164,9 @@ class Stage:
     host_rows: torch.Tensor
     device_slots: torch.Tensor
     host_slots: torch.Tensor
+    device_blocks: torch.Tensor
+    host_blocks: torch.Tensor
+    """Block ids of a block round, staged through pinned memory so their upload never waits."""
 
     def host_bytes(self) -> np.ndarray:
         """The pinned rows as bytes (a view, no copy)."""
@@ -277,6 +295,12 @@ class StepStager:
                                 sorted(g.filled))
             job.gathered = self._event()
             self._ext.event_record(job.gathered, cur)
+        self._enqueue(job, t0)
+
+    def _enqueue(self, job: StagedJob, t0: float) -> None:
+        """Hand ``job`` to the copy thread, first waiting for the oldest step when ``depth``
+        are in flight."""
+        step = job.step
         with self._in_flight_lock:
             oldest = min(self._in_flight) if len(self._in_flight) >= self._depth else None
         if oldest is not None:
@@ -289,6 +313,55 @@ class StepStager:
         self._queue.put(job)
         self.stats["steps"] += 1
         self.stats["step_thread_s"] += time.perf_counter() - t0
+
+    def commit_blocks(self, epoch: int, step: int, block_ids: Sequence[int],
+                      committed_tokens: Mapping | None = None) -> int:
+        """Stage every slot of ``block_ids``, every layer and held head, as one step.
+
+        This is a notice round's copy (core/everserve/reference/staging.py:51-94 chooses the
+        ids). It is one ``evs_gather_blocks`` launch behind the current stream's work. The
+        kernel writes the slot ids ``block * block_size + [0, block_size)`` beside the rows, and
+        they become the descriptor's slots. Returns the slots staged.
+        """
+        self._check_failed()
+        if self._step is not None:
+            raise ValueError("a step's layers are marked: commit them before a block round")
+        ids = [int(b) for b in block_ids]
+        bs = self.paged.block_size
+        if any(b < 0 or b >= self.paged.num_blocks for b in ids):
+            raise ValueError(f"a block id lies outside 0..{self.paged.num_blocks}")
+        n = len(ids) * bs
+        g = None
+        if ids:
+            st = self._staging(n)
+            st.host_blocks[:len(ids)] = torch.tensor(ids, dtype=torch.int32)
+            st.device_blocks[:len(ids)].copy_(st.host_blocks[:len(ids)], non_blocking=True)
+            g = StepGather(n, self.heads, st, set(range(len(self.layers))))
+        t0 = time.perf_counter()
+        job = StagedJob(epoch, step, dict(committed_tokens or {}), g)
+        job.times["commit"] = t0
+        if g is not None:
+            self._kernel.gather_blocks(g.stage.device_blocks[:len(ids)], self._heads_dev,
+                                       g.stage.device_rows.data_ptr(), g.stage.capacity,
+                                       g.stage.device_slots[:n])
+            job.gathered = self._event()
+            self._ext.event_record(job.gathered, torch.cuda.current_stream(self.device))
+        self._enqueue(job, t0)
+        return n
+
+    def stage_round(self, window, block_tables: Mapping, num_computed: Mapping, epoch: int,
+                    step: int) -> list[int]:
+        """Plan a notice round with :func:`everserve_amd.state.notice.blocks_to_stage` and stage
+        its blocks; updates ``window``'s counts. Returns the block ids staged."""
+        from everserve_amd.state.notice import blocks_to_stage
+
+        ids = blocks_to_stage(block_tables, num_computed, window.staged, self.paged.block_size)
+        n = self.commit_blocks(epoch, step, ids, num_computed)
+        window.rounds += 1
+        window.blocks_copied += len(ids)
+        window.bytes_copied += n * len(self.layers) * len(self.heads) * 2 * \
+            self.paged.head_dim * self._kernel.elem
+        return ids
 
     def fence(self, step: int) -> None:
         """Wait until the sink has taken ``step``; raise if staging it failed."""
@@ -351,6 +424,8 @@ class StepStager:
             host_rows=torch.empty(nbytes, dtype=torch.uint8, pin_memory=True),
             device_slots=torch.empty(capacity, dtype=torch.long, device=self.device),
             host_slots=torch.empty(capacity, dtype=torch.long, pin_memory=True),
+            device_blocks=torch.empty(capacity, dtype=torch.int32, device=self.device),
+            host_blocks=torch.empty(capacity, dtype=torch.int32, pin_memory=True),
         )
 
     def _release(self, stage: Stage) -> None:
