@@ -362,6 +362,72 @@ def bench_restore_host(ext, steps, warmup):
     }
 
 
+# ------------------------------------------------------------------------------ slot collective
+def bench_slot(ext, steps, warmup):
+    """The slot collective's one-GPU cost per call at decode sizes (evs_slot_all_reduce).
+
+    With one GPU there is no peer, so each listed member is this same row repeated: every call
+    publishes its words and then reads real, published words once per member, and never waits
+    for a peer. A HIP graph of 50 calls is replayed, with sequence numbers advancing on the
+    device, so the figure is the kernel's, not the host's launch rate. The reference's published
+    4.21 us at 16,384 elements (4 x A100) includes NVLink transport, which is not measured here.
+    """
+    import torch
+
+    dev = torch.device("cuda", 0)
+    maxn, per_graph = 65536, 50
+    half = maxn // 2
+    ctrl_host, ctrl_dev = ext.host_alloc_mapped(ext.MAX_ROWS * ext.CTRL_WORDS * 8)
+    out = {}
+    try:
+        for push in (False, True):
+            words_buf = torch.zeros((2 * ext.MAX_ROWS if push else 2) * half, dtype=torch.int64,
+                                    device=dev)
+            bufs = torch.tensor([words_buf.data_ptr()] * ext.MAX_ROWS, dtype=torch.long,
+                                device=dev)
+            for k in (1, 4, 8):
+                order = torch.tensor([k] + [0] * ext.MAX_ROWS, dtype=torch.int32, device=dev)
+                for n in (2048, 16384, 65536):
+                    x = torch.randn(n, device=dev).to(torch.bfloat16)
+                    y = torch.empty_like(x)
+                    seqs = torch.zeros(ext.slot_blocks(maxn, 1) + 1, dtype=torch.long,
+                                       device=dev)
+                    side = torch.cuda.Stream(device=dev)
+                    side.wait_stream(torch.cuda.current_stream(dev))
+                    with torch.cuda.stream(side):
+                        for _ in range(3):  # eager warmup on the capture stream
+                            ext.slot_all_reduce(x, y, bufs, ctrl_dev, order, seqs, 0, maxn, 1,
+                                                push)
+                    torch.cuda.synchronize()
+                    g = torch.cuda.CUDAGraph()
+                    with torch.cuda.graph(g, stream=side):
+                        for _ in range(per_graph):
+                            ext.slot_all_reduce(x, y, bufs, ctrl_dev, order, seqs, 0, maxn, 1,
+                                                push)
+                    for _ in range(max(1, warmup)):
+                        g.replay()
+                    torch.cuda.synchronize()
+                    reps = max(4, steps)
+                    t0 = torch.cuda.Event(enable_timing=True)
+                    t1 = torch.cuda.Event(enable_timing=True)
+                    t0.record()
+                    for _ in range(reps):
+                        g.replay()
+                    t1.record()
+                    torch.cuda.synchronize()
+                    us = t0.elapsed_time(t1) * 1e3 / (reps * per_graph)
+                    # k copies of x summed in fp32 are k * x exactly; one rounding to bf16
+                    exact = bool(torch.equal(y, (x.float() * k).to(torch.bfloat16)))
+                    out[f"{'push' if push else 'pull'}_k{k}_n{n}"] = {"us": round(us, 2),
+                                                                       "sum_exact": exact}
+                    del g
+    finally:
+        torch.cuda.synchronize()
+        ext.host_free(ctrl_host)
+    return {"config": "one GPU, members = this row repeated k times, 1 word per thread, "
+                      "graph of 50 calls replayed", "per_call": out}
+
+
 # ------------------------------------------------------------------------------ C5 reduce
 def bench_c5(ext, steps, warmup):
     import torch
@@ -651,7 +717,8 @@ def main(argv=None):
     if not a.quick:
         for name, fn in (("c3_fp8_gather_d2h", bench_c3), ("c4_restore", bench_c4),
                          ("restore_host_path", bench_restore_host),
-                         ("c5_reduce", bench_c5), ("decode_overhead", bench_decode_overhead)):
+                         ("c5_reduce", bench_c5), ("slot_all_reduce", bench_slot),
+                         ("decode_overhead", bench_decode_overhead)):
             log(f"{name} ...")
             result["extra"][name] = fn(ext, a.steps, a.warmup)
     if not a.no_cpu:

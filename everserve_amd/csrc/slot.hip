@@ -67,13 +67,14 @@ __device__ __forceinline__ uint32_t to_bf16(float f) {
   return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
 }
 
-// The address of member m's words as this member reads them, for this call's parity.
+// The address of member m's words as this member reads them; parity_off is (seq & 1) * maxn2,
+// the word offset of this call's half.
 template <bool kPush>
-__device__ __forceinline__ const uint64_t* words_of(const SlotArgs& a, int m, size_t parity) {
+__device__ __forceinline__ const uint64_t* words_of(const SlotArgs& a, int m, size_t parity_off) {
   if (kPush)
-    return reinterpret_cast<const uint64_t*>(a.bufs[a.my]) + parity * kMaxRows +
+    return reinterpret_cast<const uint64_t*>(a.bufs[a.my]) + parity_off * kMaxRows +
            static_cast<size_t>(m) * a.maxn2;
-  return reinterpret_cast<const uint64_t*>(a.bufs[m]) + parity;
+  return reinterpret_cast<const uint64_t*>(a.bufs[m]) + parity_off;
 }
 
 template <int W, bool kPush>
@@ -95,14 +96,14 @@ __global__ __launch_bounds__(kSlotThreads) void slot_all_reduce(SlotArgs a) {
   }
   __syncthreads();
   const uint32_t seq = s_seq;
-  const size_t parity = static_cast<size_t>(seq & 1u) * static_cast<size_t>(a.maxn2);
+  const size_t parity_off = static_cast<size_t>(seq & 1u) * static_cast<size_t>(a.maxn2);
   const int nmem = s_n;
   const int b0 = blockIdx.x * W * kSlotThreads + threadIdx.x;
   const uint64_t tag = static_cast<uint64_t>(seq) << 32;
 
   // publish this member's words
   if (kPush) {
-    const size_t at = parity * kMaxRows + static_cast<size_t>(a.my) * a.maxn2;
+    const size_t at = parity_off * kMaxRows + static_cast<size_t>(a.my) * a.maxn2;
     for (int q = 0; q < nmem; q++) {
       if (s_order[q] < 0) continue;
       uint64_t* dst = reinterpret_cast<uint64_t*>(a.bufs[s_order[q]]) + at;
@@ -113,7 +114,7 @@ __global__ __launch_bounds__(kSlotThreads) void slot_all_reduce(SlotArgs a) {
       }
     }
   } else {
-    uint64_t* mine = reinterpret_cast<uint64_t*>(a.bufs[a.my]) + parity;
+    uint64_t* mine = reinterpret_cast<uint64_t*>(a.bufs[a.my]) + parity_off;
 #pragma unroll
     for (int j = 0; j < W; j++) {
       const int i = b0 + j * kSlotThreads;
@@ -152,7 +153,7 @@ __global__ __launch_bounds__(kSlotThreads) void slot_all_reduce(SlotArgs a) {
 #pragma unroll
       for (int q = 0; q < kBatch; q++) {
         if (!todo[q]) continue;
-        const uint64_t* p = words_of<kPush>(a, ms[q], parity) + b0;
+        const uint64_t* p = words_of<kPush>(a, ms[q], parity_off) + b0;
 #pragma unroll
         for (int j = 0; j < W; j++)
           if (todo[q] >> j & 1) w[q][j] = load_sys(p + j * kSlotThreads);
@@ -184,7 +185,7 @@ __global__ __launch_bounds__(kSlotThreads) void slot_all_reduce(SlotArgs a) {
             for (int q = b + nm; q < nmem; q++) {
               const int m = s_order[q];
               if (m < 0) continue;
-              if (static_cast<uint32_t>(load_sys(words_of<kPush>(a, m, parity) + b0) >> 32) != seq)
+              if (static_cast<uint32_t>(load_sys(words_of<kPush>(a, m, parity_off) + b0) >> 32) != seq)
                 late |= int64_t{1} << m;
             }
             if (!counted) {
