@@ -15,9 +15,12 @@
 // else one element. Within a tile the words run along the staging buffer (K then V of one row,
 // row after row), so a wave stores whole rows: 1 KiB contiguous for bf16 d=128. For the gather
 // the tile numbers run through a slot range's head groups first, so the workgroups reading the
-// heads of one cache block (adjacent in every paged layout) run side by side. Tiles are kept
-// small (a few KiB) and numerous: on MI355X many short independent workgroups keep more bytes in
-// flight than fewer long ones (measured; a persistent grid with prefetched indices was slower).
+// heads of one cache block (adjacent in every paged layout) are neighbours; the XCD remap
+// (xcd_tile) then keeps runs of 64 neighbouring tiles on one XCD, where round-robin dealing would
+// put each on another. Tiles are kept small (a few KiB) and numerous: on MI355X many short
+// independent workgroups keep more bytes in flight than fewer long ones. Measured and rejected:
+// a persistent grid with prefetched indices, and an LDS-staged transpose that reads a tile in
+// cache order and writes it in staging order (both slower on every config).
 
 #include "common.hpp"
 
@@ -26,21 +29,37 @@ namespace {
 
 // Tuning, chosen by measurement on MI355X (the defaults); the macros let a sweep build variants
 // side by side.
-#ifndef EVS_ROWS_THREADS
-#define EVS_ROWS_THREADS 128
+#ifndef EVS_GATHER_THREADS
+#define EVS_GATHER_THREADS 256
+#endif
+#ifndef EVS_SCATTER_THREADS
+#define EVS_SCATTER_THREADS 128
 #endif
 #ifndef EVS_ROWS_VPT
 #define EVS_ROWS_VPT 2
 #endif
-#ifndef EVS_ROWS_NT
-#define EVS_ROWS_NT 0  // bit 0: nontemporal loads, bit 1: nontemporal stores
+// Per direction, bit 0: nontemporal loads, bit 1: nontemporal stores. Every byte here is touched
+// once, so no line is worth keeping in L2 or the Infinity Cache.
+#ifndef EVS_GATHER_NT
+#define EVS_GATHER_NT 3
+#endif
+#ifndef EVS_SCATTER_NT
+#define EVS_SCATTER_NT 2
 #endif
 #ifndef EVS_ROWS_ORDER
 #define EVS_ROWS_ORDER 1  // 0: a wave covers consecutive heads of one slot; 1: whole staged rows
 #endif
-#ifndef EVS_ROWS_PERSIST
-#define EVS_ROWS_PERSIST 0  // > 0: a fixed grid of this many workgroups per CU looping over tiles
+// Workgroups are dealt to the XCDs round-robin by id, so consecutive tiles (the tiles of one cache
+// block) would each run on another XCD. The chunk per direction remaps tile numbers: 0 leaves
+// them; G > 0 gives each XCD G consecutive tiles of every run of kXcds * G; -1 gives each XCD one
+// contiguous range of the whole grid.
+#ifndef EVS_GATHER_XCD_CHUNK
+#define EVS_GATHER_XCD_CHUNK 64
 #endif
+#ifndef EVS_SCATTER_XCD_CHUNK
+#define EVS_SCATTER_XCD_CHUNK 64
+#endif
+constexpr uint32_t kXcds = 8;
 // Tile shape per direction: words a tile aims at, heads it covers (0: all), head groups fastest.
 #ifndef EVS_GATHER_TILE_WORDS
 #define EVS_GATHER_TILE_WORDS 512
@@ -61,15 +80,16 @@ namespace {
 #define EVS_SCATTER_GROUP_FASTEST 0
 #endif
 
-constexpr int kThreads = EVS_ROWS_THREADS;
 constexpr int kVpt = EVS_ROWS_VPT;  // words per thread per pass, all loads issued before stores
 constexpr int kMaxTileSlots = 64;
 constexpr int kMaxHeads = 256;      // LDS table of head offsets
-constexpr int kPersist = EVS_ROWS_PERSIST;
-constexpr bool kNtLoad = (EVS_ROWS_NT & 1) != 0;
-constexpr bool kNtStore = (EVS_ROWS_NT & 2) != 0;
 
 enum Dir : int { kGather = 0, kScatter = 1 };
+
+constexpr int threads_of(int d) { return d == kGather ? EVS_GATHER_THREADS : EVS_SCATTER_THREADS; }
+constexpr int nt_of(int d) { return d == kGather ? EVS_GATHER_NT : EVS_SCATTER_NT; }
+static_assert(threads_of(kGather) >= kMaxTileSlots && threads_of(kScatter) >= kMaxTileSlots,
+              "the first TS threads fill a tile's slot offsets: a workgroup needs kMaxTileSlots");
 enum Index : int { kBySlots = 0, kByBlocks = 1 };
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -92,6 +112,7 @@ struct RowsArgs {
   int HG;                     // heads per tile (a tile's heads are HG consecutive of `heads`)
   int TS;                     // slots per tile
   int group_fastest;          // tile numbers run through head groups first
+  int xcd_chunk;              // tiles per XCD per run (see xcd_tile)
   uint32_t tile_words;        // TS * HG * 2 * W
   FastDiv div_w;              // words per half-row
   FastDiv div_h;              // heads per tile
@@ -100,18 +121,26 @@ struct RowsArgs {
   FastDiv div_groups;         // head groups
 };
 
+// Every address these kernels touch is global memory (device, or host memory mapped for the
+// device), but the cache's come out of a table of integers, so the compiler would emit flat
+// accesses; the casts to address space 1 make them global ones.
 template <typename T>
+using global_ptr = __attribute__((address_space(1))) T*;
+
+template <typename T, bool kNt>
 __device__ __forceinline__ T load_word(const char* p) {
-  if (kNtLoad) return __builtin_nontemporal_load(reinterpret_cast<const T*>(p));
-  return *reinterpret_cast<const T*>(p);
+  const global_ptr<const T> g = (global_ptr<const T>)(p);
+  if (kNt) return __builtin_nontemporal_load(g);
+  return *g;
 }
 
-template <typename T>
+template <typename T, bool kNt>
 __device__ __forceinline__ void store_word(char* p, T v) {
-  if (kNtStore)
-    __builtin_nontemporal_store(v, reinterpret_cast<T*>(p));
+  const global_ptr<T> g = (global_ptr<T>)(p);
+  if (kNt)
+    __builtin_nontemporal_store(v, g);
   else
-    *reinterpret_cast<T*>(p) = v;
+    *g = v;
 }
 
 __device__ __forceinline__ int64_t block_of(int64_t s, const RowsArgs& a) {
@@ -126,6 +155,25 @@ __device__ __forceinline__ int64_t offset_in_block(int64_t s, const RowsArgs& a)
 struct TileId {
   uint32_t layer, group, tile;
 };
+
+// The tile workgroup id b runs, ids being dealt to kXcds XCDs round-robin (x = b % kXcds).
+//   chunk > 0: in each run of kXcds * chunk ids, XCD x takes tiles [x chunk, (x + 1) chunk) of the
+//              run; a last partial run keeps its ids;
+//   chunk < 0: XCD x takes the contiguous tiles [x (q + 1), ...) when x < r, after them q each,
+//              for grid = kXcds q + r.
+// Both are bijections of [0, grid).
+__device__ __forceinline__ uint32_t xcd_tile(uint32_t b, uint32_t grid, int chunk) {
+  if (chunk == 0) return b;
+  const uint32_t x = b % kXcds, local = b / kXcds;
+  if (chunk > 0) {
+    const uint32_t run = kXcds * static_cast<uint32_t>(chunk);
+    if (b >= grid / run * run) return b;
+    const uint32_t g = static_cast<uint32_t>(chunk);
+    return (b / run) * run + x * g + local % g;
+  }
+  const uint32_t q = grid / kXcds, r = grid % kXcds;
+  return x < r ? x * (q + 1) + local : r * (q + 1) + (x - r) * q + local;
+}
 
 __device__ __forceinline__ TileId tile_id(const RowsArgs& a, uint32_t b) {
   TileId id;
@@ -147,14 +195,16 @@ __device__ __forceinline__ TileId tile_id(const RowsArgs& a, uint32_t b) {
 template <int D, int I>
 __device__ __forceinline__ int64_t slot_offset(const RowsArgs& a, uint32_t layer, int64_t t) {
   if (t >= a.n) return -1;
-  int64_t s;
   if (I == kByBlocks) {
-    const int64_t blk = a.blocks[a.bs_shift >= 0 ? (t >> a.bs_shift) : t / a.bs];
-    s = blk * a.bs + offset_in_block(t, a);
-    if (a.slots_out != nullptr && layer == 0) a.slots_out[t] = s;
-  } else {
-    s = a.slots[t];
+    // row t is offset t % bs of the (t / bs)-th listed block: no slot id to split again
+    const int64_t q = block_of(t, a);
+    const int64_t r = t - q * a.bs;
+    const int64_t blk = a.blocks[q];
+    if (a.slots_out != nullptr && layer == 0) a.slots_out[t] = blk * a.bs + r;
+    if (blk < 0) return D == kGather ? 0 : -1;  // as a negative slot id
+    return blk * a.sb + r * a.so;
   }
+  int64_t s = a.slots[t];
   if (s < 0) s = (D == kGather) ? 0 : -1;
   return s >= 0 ? block_of(s, a) * a.sb + offset_in_block(s, a) * a.so : -1;
 }
@@ -170,6 +220,7 @@ __device__ __forceinline__ void move_tile(const RowsArgs& a, const int64_t* s_sl
   char* cache_w = reinterpret_cast<char*>(a.layer_ptrs[layer]);
   char* rows_l = a.rows + static_cast<int64_t>(layer) * a.H * a.cap * (2 * a.half_bytes);
 
+  constexpr int kThreads = threads_of(D);
   for (uint32_t v0 = 0; v0 < a.tile_words; v0 += kThreads * kVpt) {
     T w[kVpt];
     int64_t cache_off[kVpt];
@@ -199,83 +250,32 @@ __device__ __forceinline__ void move_tile(const RowsArgs& a, const int64_t* s_sl
 #pragma unroll
     for (int i = 0; i < kVpt; i++) {
       if (!live[i]) continue;
-      w[i] = D == kGather ? load_word<T>(cache_base + cache_off[i])
-                          : load_word<T>(rows_l + rows_off[i]);
+      w[i] = load_word<T, (nt_of(D) & 1) != 0>(D == kGather ? cache_base + cache_off[i]
+                                                            : rows_l + rows_off[i]);
     }
 #pragma unroll
     for (int i = 0; i < kVpt; i++) {
       if (!live[i]) continue;
-      if (D == kGather)
-        store_word<T>(rows_l + rows_off[i], w[i]);
-      else
-        store_word<T>(cache_w + cache_off[i], w[i]);
+      store_word<T, (nt_of(D) & 2) != 0>(D == kGather ? rows_l + rows_off[i]
+                                                      : cache_w + cache_off[i], w[i]);
     }
   }
 }
 
 // One tile per workgroup.
 template <typename T, int D, int I>
-__global__ __launch_bounds__(kThreads) void move_rows(RowsArgs a) {
+__global__ __launch_bounds__(threads_of(D)) void move_rows(RowsArgs a) {
   __shared__ int64_t s_slot[kMaxTileSlots];  // byte offset of a slot's row in a layer, -1: none
   __shared__ int64_t s_head[kMaxHeads];      // byte offset of a head slot in a row group
 
-  const TileId id = tile_id(a, blockIdx.x);
+  const TileId id = tile_id(a, xcd_tile(blockIdx.x, gridDim.x, a.xcd_chunk));
   const int tid = threadIdx.x;
   const int64_t t0 = static_cast<int64_t>(id.tile) * a.TS;
   if (tid < a.TS) s_slot[tid] = slot_offset<D, I>(a, id.layer, t0 + tid);
   const int h0 = static_cast<int>(id.group) * a.HG;
-  for (int h = tid; h < a.HG && h0 + h < a.H; h += kThreads) s_head[h] = a.heads[h0 + h] * a.sh;
+  for (int h = tid; h < a.HG && h0 + h < a.H; h += threads_of(D)) s_head[h] = a.heads[h0 + h] * a.sh;
   __syncthreads();
   move_tile<T, D>(a, s_slot, s_head, id.layer, id.group, t0);
-}
-
-// A fixed grid of workgroups, each looping over tiles gridDim.x apart. The next tile's slot
-// offsets are read while the current tile's words move, into the other half of a double buffer,
-// so the index latency hides behind the data instead of preceding it.
-template <typename T, int D, int I>
-__global__ __launch_bounds__(kThreads) void move_rows_loop(RowsArgs a, uint32_t total_tiles) {
-  __shared__ int64_t s_slot[2][kMaxTileSlots];
-  __shared__ int64_t s_head[kMaxHeads];
-  const int tid = threadIdx.x;
-  // the loop keeps every head of the call in LDS (its tiles span all of them)
-  for (int h = tid; h < a.H; h += kThreads) s_head[h] = a.heads[h] * a.sh;
-  uint32_t tile = blockIdx.x;
-  if (tid < a.TS && tile < total_tiles) {
-    const TileId id = tile_id(a, tile);
-    s_slot[0][tid] = slot_offset<D, I>(a, id.layer, static_cast<int64_t>(id.tile) * a.TS + tid);
-  }
-  __syncthreads();
-  int buf = 0;
-  for (; tile < total_tiles; tile += gridDim.x) {
-    const uint32_t next = tile + gridDim.x;
-    int64_t next_off = -1;
-    if (tid < a.TS && next < total_tiles) {
-      const TileId nid = tile_id(a, next);
-      next_off = slot_offset<D, I>(a, nid.layer, static_cast<int64_t>(nid.tile) * a.TS + tid);
-    }
-    const TileId id = tile_id(a, tile);
-    move_tile<T, D>(a, s_slot[buf], s_head + id.group * a.HG, id.layer, id.group,
-                    static_cast<int64_t>(id.tile) * a.TS);
-    if (tid < a.TS) s_slot[buf ^ 1][tid] = next_off;
-    __syncthreads();
-    buf ^= 1;
-  }
-}
-
-int g_cus[64];
-
-int cu_count(int* cus) {
-  int dev = 0;
-  EVS_HIP(hipGetDevice(&dev));
-  EVS_REQUIRE(dev >= 0 && dev < 64, "device %d out of range", dev);
-  if (g_cus[dev] == 0) {
-    int n = 0;
-    EVS_HIP(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev));
-    EVS_REQUIRE(n > 0, "device %d reports no compute units", dev);
-    g_cus[dev] = n;
-  }
-  *cus = g_cus[dev];
-  return EVS_OK;
 }
 
 struct RowsCall {
@@ -302,6 +302,7 @@ int launch_typed(RowsArgs a, int64_t L, uint32_t W, hipStream_t stream, const ch
   const int hpt = D == kGather ? EVS_GATHER_HEADS_PER_TILE : EVS_SCATTER_HEADS_PER_TILE;
   a.HG = (hpt > 0 && hpt < a.H) ? hpt : a.H;
   a.group_fastest = D == kGather ? EVS_GATHER_GROUP_FASTEST : EVS_SCATTER_GROUP_FASTEST;
+  a.xcd_chunk = D == kGather ? EVS_GATHER_XCD_CHUNK : EVS_SCATTER_XCD_CHUNK;
   const int64_t groups = (a.H + a.HG - 1) / a.HG;
   const int64_t per_slot = static_cast<int64_t>(a.HG) * 2 * W;
   int64_t ts = target / per_slot;
@@ -320,17 +321,8 @@ int launch_typed(RowsArgs a, int64_t L, uint32_t W, hipStream_t stream, const ch
   a.div_ts = FastDiv(static_cast<uint32_t>(ts));
   a.div_tiles = FastDiv(static_cast<uint32_t>(tiles));
   a.div_groups = FastDiv(static_cast<uint32_t>(groups));
-  if (kPersist > 0) {
-    int cus = 0;
-    const int rc = cu_count(&cus);
-    if (rc != EVS_OK) return rc;
-    const int64_t blocks = grid < int64_t{cus} * kPersist ? grid : int64_t{cus} * kPersist;
-    hipLaunchKernelGGL((move_rows_loop<T, D, I>), dim3(static_cast<uint32_t>(blocks)),
-                       dim3(kThreads), 0, stream, a, static_cast<uint32_t>(grid));
-  } else {
-    hipLaunchKernelGGL((move_rows<T, D, I>), dim3(static_cast<uint32_t>(grid)), dim3(kThreads), 0,
-                       stream, a);
-  }
+  hipLaunchKernelGGL((move_rows<T, D, I>), dim3(static_cast<uint32_t>(grid)),
+                     dim3(threads_of(D)), 0, stream, a);
   EVS_LAUNCHED(name);
   return EVS_OK;
 }
