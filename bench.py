@@ -432,6 +432,8 @@ def bench_slot(ext, steps, warmup):
 def bench_c5(ext, steps, warmup):
     import torch
 
+    from everserve_amd.kernels import REDUCE_STATE_WORDS
+
     K, N, SETS = 8, 256 * 8192, 8
     dev = torch.device("cuda", 0)
     stream = torch.cuda.current_stream(dev)
@@ -445,7 +447,7 @@ def bench_c5(ext, steps, warmup):
         sets.append((bufs, table, out))
     flags = torch.full((8,), 1, dtype=torch.long, device=dev)
     order = torch.tensor([K, *range(K)], dtype=torch.int32, device=dev)
-    state = torch.zeros(4, dtype=torch.long, device=dev)
+    state = torch.zeros(REDUCE_STATE_WORDS, dtype=torch.long, device=dev)
     it = [0]
 
     def reduce_once():
@@ -652,6 +654,8 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="the headline only, no other configs")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--legs", default="",
+                    help="comma-separated extra legs to run (default: all; --quick: none)")
     ap.add_argument("--pmc", action="store_true",
                     help="only the counter runs' workload (5 gathers, 5 calibration copies)")
     a = ap.parse_args(argv)
@@ -714,11 +718,18 @@ def main(argv=None):
         result["extra"]["c2_gather_blocks"] = {
             "ms": round(bms, 4), "gbs": round(c2["algo_bytes"] / bms / 1e6, 1),
             "rows_equal_gather_rows": c2["blocks_equal"]}
+    legs = (("c3_fp8_gather_d2h", bench_c3), ("c4_restore", bench_c4),
+            ("restore_host_path", bench_restore_host), ("c5_reduce", bench_c5),
+            ("slot_all_reduce", bench_slot), ("decode_overhead", bench_decode_overhead))
+    wanted = {x for x in a.legs.split(",") if x}
+    unknown = wanted - {name for name, _ in legs}
+    if unknown:
+        print(f"unknown legs: {sorted(unknown)}", file=sys.stderr)
+        return 2
     if not a.quick:
-        for name, fn in (("c3_fp8_gather_d2h", bench_c3), ("c4_restore", bench_c4),
-                         ("restore_host_path", bench_restore_host),
-                         ("c5_reduce", bench_c5), ("slot_all_reduce", bench_slot),
-                         ("decode_overhead", bench_decode_overhead)):
+        for name, fn in legs:
+            if wanted and name not in wanted:
+                continue
             log(f"{name} ...")
             result["extra"][name] = fn(ext, a.steps, a.warmup)
     if not a.no_cpu:

@@ -15,21 +15,36 @@
 // missing then contributes zeros, as the reference's aborted reads do (slot.cu:148). Past the
 // BOUND control word (ns, 0 = off) the workgroup writes the rows it still waits for into LATE,
 // and the last workgroup that named clears LATE once its wait is over (slot.cu:29-40,174-214).
+// Every workgroup is resident at once and bounds its own wait by ABORT and the clock, so they
+// give up together, within the skew of their starts.
 //
 // The call's outcome is one word, state[0] = (epoch << 16) | (reason << 8) | late rows, written by
-// the last workgroup to finish. Completion is counted in one word, state[1]: each workgroup ORs
-// its outcome into the high bits and then adds 1 to the low bits, both relaxed atomics on that
-// one location, whose single modification order puts every workgroup's outcome before the last
-// workgroup's add. No fence is needed, so no workgroup writes back or invalidates the L2 at its
-// end. state[1] and state[3] return to zero at the end of every call, so the launch needs no
-// memset and a captured graph can replay it.
+// the last workgroup to count. Each workgroup counts once its wait is over, before its payload:
+// the outcome is settled then, and state[0] is read only after the kernel has completed.
+// Completion is counted in two levels of words. Workgroup b counts
+// in group word x = b mod G (G = min(8, workgroups), the words 256 bytes apart): it ORs its
+// outcome into the high bits and then adds 1 to the low bits, both relaxed atomics on that one
+// location, whose single modification order puts every outcome of the group before the last
+// add. The group's last workgroup carries the group's outcome the same way into the top word,
+// state[1], whose last adder then writes state[0]. No fence is needed, so no workgroup writes back
+// or invalidates the L2; and no word takes more than ceil(workgroups / G) + G of the atomics,
+// which on MI355X serialise per address at device scope (one word for every workgroup cost
+// 2.8 us of a 13 us call at 256 workgroups). The counting words return to zero at the end of
+// every call, so the launch needs no memset and a captured graph can replay it.
 
 #include "common.hpp"
 
 namespace evs {
 namespace {
 
-constexpr int kThreads = 256;
+#ifndef EVS_REDUCE_THREADS
+#define EVS_REDUCE_THREADS 256
+#endif
+// bit 0: nontemporal payload loads, bit 1: nontemporal output stores (each byte is touched once)
+#ifndef EVS_REDUCE_NT
+#define EVS_REDUCE_NT 3
+#endif
+constexpr int kThreads = EVS_REDUCE_THREADS;
 constexpr int kMaxRows = EVS_MAX_ROWS;
 #ifndef EVS_REDUCE_VPT
 #define EVS_REDUCE_VPT 4
@@ -41,7 +56,10 @@ constexpr int kVpt = EVS_REDUCE_VPT;  // 8-element vectors per thread per pass
 constexpr int kMaxBlocks = EVS_REDUCE_MAX_BLOCKS;  // all resident on 256 CUs: each polls once
 constexpr int kPollsPerCheck = 32; // flag polls between clock and ABORT reads
 constexpr int kBadOrder = 4;       // reason bit: `order` named a row outside [0, MAX_ROWS)
-constexpr int kDoneBits = 20;      // state[1]: workgroups done in bits [0, 20), outcome above
+constexpr int kDoneBits = 20;      // counting words: workgroups done in bits [0, 20), outcome above
+constexpr uint32_t kGroups = 8;    // group counting words
+constexpr int kGroupStride = 32;   // words between counting words (256 bytes)
+static_assert(kGroupStride * (1 + kGroups) <= EVS_REDUCE_STATE_WORDS, "state record too small");
 
 // How the payload reads are ordered after the flags. 3 (default): every payload load is a buffer
 // load at agent scope (sc1), coherent on its own, so no cache is invalidated; issued after the
@@ -51,7 +69,8 @@ constexpr int kDoneBits = 20;      // state[1]: workgroups done in bits [0, 20),
 #ifndef EVS_REDUCE_FENCE
 #define EVS_REDUCE_FENCE 3
 #endif
-constexpr int kPayloadScope = 16;  // buffer-load cache policy: sc1, coherent at agent scope
+// buffer-load cache policy: sc1 (coherent at agent scope), plus nt when the payload streams
+constexpr int kPayloadScope = 16 | ((EVS_REDUCE_NT & 1) ? 2 : 0);
 constexpr int kRsrcWord3 = 0x00020000;  // raw buffer resource, dword 3 (gfx9 untyped access)
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -91,6 +110,25 @@ __device__ __forceinline__ uint32_t f32_to_bf16(float f) {
   return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
 }
 
+// Count one arrival with `outcome` in the counting word w: OR the outcome into the high bits, then
+// add 1 to the low bits. Returns the word as it was before the add.
+__device__ __forceinline__ uint64_t arrive(uint64_t* w, uint64_t outcome) {
+  if (outcome != 0)
+    __hip_atomic_fetch_or(w, outcome << kDoneBits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return __hip_atomic_fetch_add(w, uint64_t{1}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Whether the arrival that saw `before` was the last of `arrivals`. The last one gets every
+// arrival's outcome in `all` and returns w to zero (the next call touches it only after this
+// kernel has ended).
+__device__ __forceinline__ bool last(uint64_t* w, uint64_t before, uint32_t arrivals,
+                                     uint64_t& all) {
+  if ((before & ((uint64_t{1} << kDoneBits) - 1)) != arrivals - 1) return false;
+  all = (before >> kDoneBits) & 0xffffu;
+  __hip_atomic_store(w, uint64_t{0}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return true;
+}
+
 __global__ __launch_bounds__(kThreads) void local_reduce(ReduceArgs a) {
   __shared__ const uint16_t* s_src[kMaxRows];  // member in order position q, or null: missing
   __shared__ int s_count;
@@ -125,17 +163,12 @@ __global__ __launch_bounds__(kThreads) void local_reduce(ReduceArgs a) {
       for (uint64_t poll = 0;; ++poll) {
         if (poll % kPollsPerCheck == kPollsPerCheck - 1) {
           const int64_t waited = wall_clock64() - t0;
-          uint64_t abort = 0, given_up = 0, bound_ns = 0;
-          if (lane == 0) {
-            if (a.ctrl != nullptr) {
-              abort = load_system(reinterpret_cast<const uint64_t*>(a.ctrl + EVS_ABORT));
-              bound_ns = load_system(reinterpret_cast<const uint64_t*>(a.ctrl + EVS_BOUND));
-            }
-            given_up = __hip_atomic_load(a.state + 1, __ATOMIC_RELAXED,
-                                         __HIP_MEMORY_SCOPE_AGENT) >> (kDoneBits + 8);
+          uint64_t abort = 0, bound_ns = 0;
+          if (lane == 0 && a.ctrl != nullptr) {
+            abort = load_system(reinterpret_cast<const uint64_t*>(a.ctrl + EVS_ABORT));
+            bound_ns = load_system(reinterpret_cast<const uint64_t*>(a.ctrl + EVS_BOUND));
           }
           abort = __shfl(abort, 0);
-          given_up = __shfl(given_up, 0);
           bound_ns = __shfl(bound_ns, 0);
           // rows this workgroup still waits for
           uint32_t rows = (missing >> lane) & 1 ? (1u << row) : 0u;
@@ -155,10 +188,6 @@ __global__ __launch_bounds__(kThreads) void local_reduce(ReduceArgs a) {
           }
           if (abort != 0) {
             reason |= EVS_REDUCE_ABORTED;
-            break;
-          }
-          if (given_up != 0) {
-            reason |= static_cast<uint32_t>(given_up) & (EVS_REDUCE_ABORTED | EVS_REDUCE_TIMED_OUT);
             break;
           }
           if (waited > a.timeout_ticks || poll >= a.max_polls) {
@@ -197,6 +226,14 @@ __global__ __launch_bounds__(kThreads) void local_reduce(ReduceArgs a) {
   }
   __syncthreads();
   if (EVS_REDUCE_FENCE == 2) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  // This workgroup's outcome is settled once its wait is over, so it is counted now: the
+  // counting atomic's round trip then overlaps the payload instead of following it. state[0] is
+  // read only once the kernel has completed, when every workgroup's payload is written too.
+  const uint32_t groups = gridDim.x < kGroups ? gridDim.x : kGroups;
+  const uint32_t group = blockIdx.x % groups;
+  uint64_t* const group_word = a.state + kGroupStride * (1 + group);
+  uint64_t group_before = 0;
+  if (tid == 0) group_before = arrive(group_word, s_outcome);
 
   const int count = s_count;
   const int64_t nvec = s_vectors ? a.nvec : 0;
@@ -260,7 +297,10 @@ __global__ __launch_bounds__(kThreads) void local_reduce(ReduceArgs a) {
       u32x4 y;
 #pragma unroll
       for (int w = 0; w < 4; w++) y[w] = f32_to_bf16(acc[2 * w]) | (f32_to_bf16(acc[2 * w + 1]) << 16);
-      *reinterpret_cast<u32x4*>(a.out + v * 8) = y;
+      if (EVS_REDUCE_NT & 2)
+        __builtin_nontemporal_store(y, reinterpret_cast<u32x4*>(a.out + v * 8));
+      else
+        *reinterpret_cast<u32x4*>(a.out + v * 8) = y;
     }
   }
   // the elements the vectors do not cover: a tail of fewer than 8, or all of them when a buffer
@@ -281,18 +321,12 @@ __global__ __launch_bounds__(kThreads) void local_reduce(ReduceArgs a) {
   }
 
   if (tid == 0) {
-    const uint64_t outcome = s_outcome;
-    if (outcome != 0)
-      __hip_atomic_fetch_or(a.state + 1, outcome << kDoneBits, __ATOMIC_RELAXED,
-                            __HIP_MEMORY_SCOPE_AGENT);
-    const uint64_t before = __hip_atomic_fetch_add(a.state + 1, uint64_t{1}, __ATOMIC_RELAXED,
-                                                   __HIP_MEMORY_SCOPE_AGENT);
-    if ((before & ((uint64_t{1} << kDoneBits) - 1)) == gridDim.x - 1) {
-      // the last workgroup: every other one's outcome is in the word it just added to; the
-      // next call's workgroups touch it only after this kernel has ended
-      const uint64_t all = (before >> kDoneBits) & 0xffffu;
-      __hip_atomic_store(a.state + 1, uint64_t{0}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(a.state + 0, (a.epoch << 16) | all, __ATOMIC_RELAXED,
+    const uint32_t in_group = (gridDim.x - group + groups - 1) / groups;  // ids b, b % groups == group
+    uint64_t outcome = 0;
+    if (last(group_word, group_before, in_group, outcome) &&
+        last(a.state + 1, arrive(a.state + 1, outcome), groups, outcome)) {
+      // the last workgroup of the call: every outcome is in `outcome`
+      __hip_atomic_store(a.state + 0, (a.epoch << 16) | outcome, __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_SYSTEM);
     }
   }

@@ -47,6 +47,9 @@ _PACKAGE = Path(__file__).resolve().parent
 EVS_OK = 0
 
 
+REDUCE_STATE_WORDS = 288
+"""64-bit words of local_reduce's state record (EVS_REDUCE_STATE_WORDS in the C header)."""
+
 class KernelsUnavailable(RuntimeError):
     """The kernels cannot be loaded here, and why: a wrong or stale build, no GPU."""
 
@@ -369,7 +372,8 @@ class Kernels:
 
         ``bufs`` int64 [MAX_ROWS] addresses, ``flags`` 64-bit [MAX_ROWS] (a tensor, or the
         device address of host-mapped words), ``order`` int32
-        [1 + MAX_ROWS] = [count, rows...], ``state`` 64-bit [4] (zeroed once): all on the device.
+        [1 + MAX_ROWS] = [count, rows...], ``state`` 64-bit [REDUCE_STATE_WORDS] (zeroed once):
+        all on the device.
         ``ctrl_ptr`` is the device address of this member's control row (0: none). The wait ends
         at the ABORT word or after ``timeout_ns``; the outcome is in ``state[0]``.
         """
@@ -387,8 +391,10 @@ class Kernels:
         op = _device_ptr(order, "local_reduce: order", torch.int32)
         if order.numel() != 1 + self.MAX_ROWS or bufs.numel() < self.MAX_ROWS:
             raise RuntimeError("local_reduce: order is int32 [1 + MAX_ROWS], bufs [MAX_ROWS]")
-        if state.element_size() != 8 or state.numel() < 4 or not state.is_cuda:
-            raise RuntimeError("local_reduce: state is four 64-bit words on the device")
+        if (state.element_size() != 8 or state.numel() < REDUCE_STATE_WORDS or not state.is_cuda
+                or not state.is_contiguous()):
+            raise RuntimeError(f"local_reduce: state is {REDUCE_STATE_WORDS} contiguous 64-bit "
+                               f"words on the device")
         with torch.cuda.device(out.device):
             self._check(
                 self._lib.evs_local_reduce(

@@ -44,7 +44,7 @@ extern "C" {
 #define EVS_REDUCE_DONE 0      /* every member's flag carried the call's epoch */
 #define EVS_REDUCE_ABORTED 1   /* released by the ABORT control word */
 #define EVS_REDUCE_TIMED_OUT 2 /* the hard timeout passed with members still missing */
-#define EVS_REDUCE_STATE_WORDS 4
+#define EVS_REDUCE_STATE_WORDS 288 /* state[0] the outcome; the rest the kernel's counters */
 
 /* The message of the last failed call on this thread ("" if none). */
 const char* evs_last_error(void);

@@ -73,3 +73,11 @@ def test_the_build_is_stamped_with_this_trees_sources():
     stamp = kernels._check_stamp(kernels._PACKAGE)
     assert stamp.name == kernels.LIBRARY
     assert build.stamp()["sources"] == kernels.stamp()["sources"]
+
+
+def test_the_reduce_state_size_is_the_headers():
+    from everserve_amd import kernels
+
+    header = (Path(__file__).resolve().parents[1] / "include" / "everserve_mi355x.h").read_text()
+    m = re.search(r"#define EVS_REDUCE_STATE_WORDS (\d+)", header)
+    assert m is not None and int(m.group(1)) == kernels.REDUCE_STATE_WORDS

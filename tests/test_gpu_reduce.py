@@ -18,6 +18,7 @@ import pytest
 import torch
 
 import oracle
+from everserve_amd.kernels import REDUCE_STATE_WORDS
 from tests.cases import bits
 
 pytestmark = pytest.mark.gpu
@@ -55,7 +56,7 @@ class Members:
         self.flags = torch.zeros(MAXW, dtype=torch.long, device="cuda")
         self.order = torch.tensor([len(order), *order] + [0] * (MAXW - len(order)),
                                   dtype=torch.int32, device="cuda")
-        self.state = torch.zeros(4, dtype=torch.long, device="cuda")
+        self.state = torch.zeros(REDUCE_STATE_WORDS, dtype=torch.long, device="cuda")
         n = next(iter(inputs.values())).numel()
         self.out = torch.empty(n, dtype=torch.bfloat16, device="cuda")
 
@@ -82,7 +83,7 @@ def test_the_sum_is_the_ordered_fp32_sum_bit_for_bit(ext, n, order):
     want = oracle.member_sum([bits(inputs[r]) for r in order])
     assert np.array_equal(bits(m.out), want)
     assert m.status() == (1, 0, 0)
-    assert m.state[1:].cpu().tolist() == [0, 0, 0]  # the kernel's counters are back at zero
+    assert not m.state[1:].any()  # the kernel's counters are back at zero
 
 
 def test_the_order_of_the_sum_shows_and_is_kept(ext):
@@ -213,4 +214,4 @@ def test_a_captured_reduction_replays_like_eager_calls(ext):
         torch.cuda.synchronize()
         assert np.array_equal(bits(m.out), want), i
         assert m.status() == (5, 0, 0)
-        assert m.state[1:].cpu().tolist() == [0, 0, 0]
+        assert not m.state[1:].any()
