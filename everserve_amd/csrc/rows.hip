@@ -212,12 +212,12 @@ __device__ __forceinline__ int64_t slot_offset(const RowsArgs& a, uint32_t layer
 // Move one tile's words: the slots' offsets and the heads' are in LDS.
 template <typename T, int D>
 __device__ __forceinline__ void move_tile(const RowsArgs& a, const int64_t* s_slot,
-                                          const int64_t* s_head, uint32_t layer, uint32_t group,
-                                          int64_t t0) {
+                                          const int64_t* s_head, int64_t layer_base,
+                                          uint32_t layer, uint32_t group, int64_t t0) {
   const uint32_t h0 = group * a.HG;
   const int tid = threadIdx.x;
-  const char* cache_base = reinterpret_cast<const char*>(a.layer_ptrs[layer]);
-  char* cache_w = reinterpret_cast<char*>(a.layer_ptrs[layer]);
+  const char* cache_base = reinterpret_cast<const char*>(layer_base);
+  char* cache_w = reinterpret_cast<char*>(layer_base);
   char* rows_l = a.rows + static_cast<int64_t>(layer) * a.H * a.cap * (2 * a.half_bytes);
 
   constexpr int kThreads = threads_of(D);
@@ -271,11 +271,15 @@ __global__ __launch_bounds__(threads_of(D)) void move_rows(RowsArgs a) {
   const TileId id = tile_id(a, xcd_tile(blockIdx.x, gridDim.x, a.xcd_chunk));
   const int tid = threadIdx.x;
   const int64_t t0 = static_cast<int64_t>(id.tile) * a.TS;
+  // Read before the block-table path's slot-tag store below: after a store the compiler cannot
+  // keep this uniform read scalar (the store might alias it), and a vector read of it made every
+  // pass wait for all memory operations in flight (measured 8 % slower).
+  const int64_t layer_base = a.layer_ptrs[id.layer];
   if (tid < a.TS) s_slot[tid] = slot_offset<D, I>(a, id.layer, t0 + tid);
   const int h0 = static_cast<int>(id.group) * a.HG;
   for (int h = tid; h < a.HG && h0 + h < a.H; h += threads_of(D)) s_head[h] = a.heads[h0 + h] * a.sh;
   __syncthreads();
-  move_tile<T, D>(a, s_slot, s_head, id.layer, id.group, t0);
+  move_tile<T, D>(a, s_slot, s_head, layer_base, id.layer, id.group, t0);
 }
 
 struct RowsCall {
