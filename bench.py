@@ -184,6 +184,51 @@ def cpu_baseline_c2(seconds=10.0):
     }
 
 
+def cpu_baselines_more(seconds=5.0):
+    """The reference's torch CPU path for the restore (C4, on one layer) and the reduce (C5)."""
+    import numpy as np
+    import torch
+
+    from oracle import cpu_path
+
+    threads = torch.get_num_threads()
+    out = {}
+    # C4: staged rows written back at a random permutation of whole blocks, every head slot
+    L, NB, BS, H, D = 1, 16384, 16, 8, 128
+    n = NB * BS
+    staged = torch.ones((L, H, n, 2, D), dtype=torch.bfloat16)  # a copy: the values do not matter
+    layers = [torch.zeros((2, NB, BS, H, D), dtype=torch.bfloat16) for _ in range(L)]
+    perm = np.random.default_rng(4).permutation(NB).astype(np.int64)
+    slots = torch.from_numpy((perm[:, None] * BS + np.arange(BS)[None, :]).reshape(-1))
+    heads = list(range(H))
+    reps, t0 = 0, time.perf_counter()
+    while reps == 0 or time.perf_counter() - t0 < seconds:
+        cpu_path.restore_step(layers, slots, heads, staged)
+        reps += 1
+    el = time.perf_counter() - t0
+    out["c4_restore"] = {
+        "value": round(2 * L * H * n * 2 * D * 2 * reps / el / 1e9, 3), "unit": "GB/s",
+        "cores": threads, "kind": "port",
+        "sample": f"C4 restore on 1 of 32 layers (16384-block cache, random block permutation, 8 "
+                  f"heads): index_select + write_rows per (layer, head) (mirror.py:926-937), "
+                  f"{reps} steps in {el:.1f} s"}
+    del staged, layers
+    # C5: 8 members of 2,097,152 bf16, summed in order in fp32
+    K, N = 8, 256 * 8192
+    members = [torch.randn(N, generator=torch.Generator().manual_seed(5 + i)).to(torch.bfloat16)
+               for i in range(K)]
+    reps, t0 = 0, time.perf_counter()
+    while reps == 0 or time.perf_counter() - t0 < seconds:
+        cpu_path.member_sum(members)
+        reps += 1
+    el = time.perf_counter() - t0
+    out["c5_reduce"] = {
+        "value": round(el / reps * 1e6, 1), "unit": "us per call", "cores": threads,
+        "kind": "port",
+        "sample": f"C5 member_sum of 8 x 2,097,152 bf16 (ops.py:63-73), {reps} calls in {el:.1f} s"}
+    return out
+
+
 # ------------------------------------------------------------------------------ C3 fp8 + D2H
 def bench_c3(ext, steps, warmup):
     import torch
@@ -650,7 +695,7 @@ def pmc_workload(ext, launches=5):
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="the headline only, no other configs")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -735,6 +780,9 @@ def main(argv=None):
     if not a.no_cpu:
         log("cpu baseline ...")
         result["cpu_baseline"] = cpu_baseline_c2()
+        if not a.quick and not wanted:
+            log("cpu baselines of the restore and the reduce ...")
+            result["extra"]["cpu_baselines_more"] = cpu_baselines_more()
     print(json.dumps(result), flush=True)
     return 0
 
