@@ -1,0 +1,187 @@
+"""Edge cases of the HIP path on the GPU, each against the oracle.
+
+* **Ragged counts.** Slot counts that do not fill the last tile, and capacities larger than the
+  count. Rows past the count must be left as they were: the output is pre-filled with a
+  sentinel, and the oracle gathers into the same pre-filled rows. This covers every layout, d in
+  {8, 6}, padding ids, the block gather and the scatter.
+* **Empty calls.** No slots, no heads or no layers: nothing is written, and nothing fails.
+* **The widest head table.** 256 head slots in one call; 257 is refused.
+* **The reduce's element path.** A member or the output not 16-byte aligned; lengths that are
+  not a multiple of 8; no members listed; and a length of 0, which still reports completion.
+* **fp8 e5m2** moves as raw bytes, like e4m3.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from everserve_amd.kernels import REDUCE_STATE_WORDS, KernelError
+from tests.cases import LAYOUTS, bits, caches, strides_of
+
+pytestmark = pytest.mark.gpu
+
+NB, BS, H, L = 80, 4, 3, 2
+SENTINEL = 0x5A5A
+
+
+def dev_long(xs):
+    return torch.tensor([int(x) for x in xs], dtype=torch.long, device="cuda")
+
+
+def ptrs(layers):
+    return dev_long([t.data_ptr() for t in layers])
+
+
+def ragged_slots(n: int, seed: int) -> list[int]:
+    rng = np.random.default_rng(seed)
+    s = rng.choice(NB * BS, size=n, replace=False).astype(np.int64)
+    s[rng.random(n) < 0.1] = -1  # padding ids
+    return s.tolist()
+
+
+@pytest.mark.parametrize("layout", LAYOUTS)
+@pytest.mark.parametrize("d", [8, 6])
+@pytest.mark.parametrize("n", [1, 7, 9, 63, 65, 257])
+def test_ragged_counts_leave_the_rows_past_n_alone(ext, layout, d, n):
+    layers = caches(layout, d, torch.bfloat16, n_layers=L, nb=NB, h=H, seed=n)
+    slots, heads, cap = ragged_slots(n, n), [2, 0], n + 5
+    want = np.full((L, len(heads), cap, 2, d), SENTINEL, dtype=np.uint16)
+    oracle.gather_rows(layers, slots, heads, cap, d, BS, strides_of(layers[0]), 2, out=want)
+    gpu = [t.cuda() for t in layers]
+    out = torch.full((L, len(heads), cap, 2, d), SENTINEL, dtype=torch.int16, device="cuda")
+    ext.gather_rows(ptrs(gpu), dev_long(slots), dev_long(heads), out.data_ptr(), cap, d, BS,
+                    list(strides_of(gpu[0])), 2)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy().view(np.uint16), want)
+
+
+@pytest.mark.parametrize("layout", LAYOUTS)
+@pytest.mark.parametrize("blocks", [[3], [9, 0, 77], list(range(40, 57))])
+def test_ragged_block_lists(ext, layout, blocks):
+    d = 8
+    layers = caches(layout, d, torch.bfloat16, n_layers=L, nb=NB, h=H, seed=len(blocks))
+    slots = oracle.expand_blocks(blocks, BS)
+    cap = len(slots) + 3
+    want = np.full((L, H, cap, 2, d), SENTINEL, dtype=np.uint16)
+    oracle.gather_rows(layers, slots, list(range(H)), cap, d, BS, strides_of(layers[0]), 2,
+                       out=want)
+    gpu = [t.cuda() for t in layers]
+    out = torch.full((L, H, cap, 2, d), SENTINEL, dtype=torch.int16, device="cuda")
+    tags = torch.full((len(slots),), -9, dtype=torch.long, device="cuda")
+    ext.gather_blocks(ptrs(gpu), torch.tensor(blocks, dtype=torch.int32, device="cuda"),
+                      dev_long(range(H)), out.data_ptr(), cap, d, BS, list(strides_of(gpu[0])), 2,
+                      slots_out=tags)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy().view(np.uint16), want)
+    assert tags.cpu().tolist() == slots.tolist()
+
+
+@pytest.mark.parametrize("layout", LAYOUTS)
+@pytest.mark.parametrize("n", [1, 9, 65])
+def test_ragged_scatter_writes_only_the_listed_rows(ext, layout, n):
+    d = 6
+    src = caches(layout, d, torch.bfloat16, n_layers=L, nb=NB, h=H, seed=100 + n)
+    slots, heads, cap = ragged_slots(n, 100 + n), [1, 2], n + 2
+    rows = oracle.gather_rows(src, slots, heads, cap, d, BS, strides_of(src[0]), 2)
+    dst = caches(layout, d, torch.bfloat16, n_layers=L, nb=NB, h=H, seed=200 + n)
+    want = [t.clone() for t in dst]
+    oracle.scatter_rows(want, slots, heads, rows, cap, d, BS, strides_of(want[0]), 2)
+    gpu = [t.cuda() for t in dst]
+    r = torch.from_numpy(rows.view(np.int16).copy()).cuda()
+    ext.scatter_rows(ptrs(gpu), dev_long(slots), dev_long(heads), r.data_ptr(), cap, d, BS,
+                     list(strides_of(gpu[0])), 2)
+    torch.cuda.synchronize()
+    for g, w in zip(gpu, want):
+        assert np.array_equal(bits(g), bits(w))
+
+
+def test_empty_calls_write_nothing(ext):
+    layers = [t.cuda() for t in caches("kv_first", 8, torch.bfloat16, n_layers=L, nb=NB, h=H)]
+    out = torch.full((L, H, 4, 2, 8), SENTINEL, dtype=torch.int16, device="cuda")
+    st = list(strides_of(layers[0]))
+    s, h = dev_long([3, 5]), dev_long([0, 1, 2])
+    ext.gather_rows(ptrs(layers), s[:0], h, out.data_ptr(), 4, 8, BS, st, 2)
+    ext.gather_rows(ptrs(layers), s, h[:0], out.data_ptr(), 4, 8, BS, st, 2)
+    ext.gather_rows(ptrs(layers)[:0], s, h, out.data_ptr(), 4, 8, BS, st, 2)
+    ext.scatter_rows(ptrs(layers), s[:0], h, out.data_ptr(), 4, 8, BS, st, 2)
+    ext.gather_blocks(ptrs(layers), torch.empty(0, dtype=torch.int32, device="cuda"), h,
+                      out.data_ptr(), 4, 8, BS, st, 2)
+    torch.cuda.synchronize()
+    assert bool((out == SENTINEL).all())
+
+
+def test_256_head_slots_in_one_call_and_257_refused(ext):
+    d, nb, heads = 8, 6, 256
+    g = torch.Generator().manual_seed(9)
+    layers = [torch.randn((2, nb, BS, heads, d), generator=g).to(torch.bfloat16)]
+    slots, order = [5, 0, 23, -1], list(range(heads))[::-1]
+    want = oracle.gather_rows(layers, slots, order, 4, d, BS, strides_of(layers[0]), 2)
+    gpu = [t.cuda() for t in layers]
+    out = torch.zeros(want.shape, dtype=torch.int16, device="cuda")
+    ext.gather_rows(ptrs(gpu), dev_long(slots), dev_long(order), out.data_ptr(), 4, d, BS,
+                    list(strides_of(gpu[0])), 2)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy().view(np.uint16), want)
+    with pytest.raises(KernelError, match="head slots"):
+        ext.gather_rows(ptrs(gpu), dev_long(slots), dev_long(order + [0]), out.data_ptr(), 4,
+                        d, BS, list(strides_of(gpu[0])), 2)
+
+
+def test_fp8_e5m2_moves_as_raw_bytes(ext):
+    layers = caches("blocks_first", 8, torch.float8_e5m2, n_layers=L, nb=NB, h=H, seed=4)
+    slots = ragged_slots(33, 4)
+    want = oracle.gather_rows(layers, slots, [0, 1, 2], 40, 8, BS, strides_of(layers[0]), 1)
+    gpu = [t.cuda() for t in layers]
+    out = torch.zeros(want.shape, dtype=torch.uint8, device="cuda")
+    ext.gather_rows(ptrs(gpu), dev_long(slots), dev_long([0, 1, 2]), out.data_ptr(), 40, 8, BS,
+                    list(strides_of(gpu[0])), 1)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy(), want)
+
+
+def member(rank: int, n: int) -> torch.Tensor:
+    g = torch.Generator().manual_seed(77 * rank + n)
+    return torch.randn(n, generator=g).to(torch.bfloat16)
+
+
+def reduce_call(ext, members, order, out):
+    table = dev_long([m.data_ptr() for m in members] + [0] * (8 - len(members)))
+    flags = torch.ones(8, dtype=torch.long, device="cuda")
+    o = torch.tensor([len(order), *order] + [0] * (8 - len(order)), dtype=torch.int32,
+                     device="cuda")
+    state = torch.zeros(REDUCE_STATE_WORDS, dtype=torch.long, device="cuda")
+    ext.local_reduce(table, flags, o, out, 1, 10**9, 0, state)
+    torch.cuda.synchronize()
+    assert int(state[0].item()) == 1 << 16
+    assert not state[1:].any()
+
+
+@pytest.mark.parametrize("n", [1, 7, 9, 1001])
+@pytest.mark.parametrize("misaligned", ["member", "output", "none"])
+def test_the_reduce_element_path_and_tails(ext, n, misaligned):
+    xs = [member(r, n) for r in range(3)]
+    members = []
+    for r, x in enumerate(xs):
+        if misaligned == "member" and r == 1:
+            big = torch.empty(n + 1, dtype=torch.bfloat16, device="cuda")
+            big[1:] = x.cuda()
+            members.append(big[1:])  # 2-byte aligned, not 16
+        else:
+            members.append(x.cuda())
+    if misaligned == "output":
+        out = torch.empty(n + 1, dtype=torch.bfloat16, device="cuda")[1:]
+    else:
+        out = torch.empty(n, dtype=torch.bfloat16, device="cuda")
+    order = [1, 2, 0]
+    reduce_call(ext, members, order, out)
+    assert np.array_equal(bits(out), oracle.member_sum([bits(xs[r]) for r in order]))
+
+
+def test_the_reduce_of_no_members_is_zeros_and_of_no_elements_completes(ext):
+    xs = [member(r, 4096).cuda() for r in range(2)]
+    out = torch.full((4096,), 7.0, dtype=torch.bfloat16, device="cuda")
+    reduce_call(ext, xs, [], out)
+    assert not out.any()
+    empty = torch.empty(0, dtype=torch.bfloat16, device="cuda")
+    reduce_call(ext, [x[:0] for x in xs], [0, 1], empty)
