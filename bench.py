@@ -662,33 +662,77 @@ def bench_decode_overhead(ext, steps, warmup):
 
 
 # ------------------------------------------------------------------------------ counter runs
-def pmc_workload(ext, launches=5):
-    """What the rocprofv3 counter runs measure: ``launches`` C2 gathers, then ``launches`` copies
-    of a 1 GiB bf16 tensor by an elementwise kernel (torch.neg) whose FETCH_SIZE and WRITE_SIZE
-    are known to be 1 GiB each, the scale the gather's counters are read against."""
+def pmc_workload(ext, which="gather", launches=5):
+    """What the rocprofv3 counter runs measure: ``launches`` calls of one kernel, then
+    ``launches`` copies of a 1 GiB bf16 tensor by an elementwise kernel (torch.neg) whose
+    FETCH_SIZE and WRITE_SIZE are known to be 1 GiB each, the scale the kernel's counters are
+    read against.
+
+    gather: the C2 gather. scatter: the C4 restore scatter (32 layers, 64 GiB moved).
+    reduce: the C5 local reduce, each call on another of 8 buffer sets (288 MiB in all, more
+    than the Infinity Cache holds).
+    """
     import torch
 
-    L, NB, BS, H, D = 32, 8192, 16, 8, 128
+    from everserve_amd.kernels import REDUCE_STATE_WORDS
+
     dev = torch.device("cuda", 0)
-    layers = random_cache_layers(L, (2, NB, BS, H, D), torch.bfloat16, dev, seed=0)
-    _, slots = block_table_slots(NB, 1024, BS, seed=2)
-    n = len(slots)
-    ptrs = torch.tensor([t.data_ptr() for t in layers], dtype=torch.long, device=dev)
-    s = torch.from_numpy(slots).to(dev)
-    heads = torch.arange(H, dtype=torch.long, device=dev)
-    out = torch.empty((L, H, n, 2, D), dtype=torch.bfloat16, device=dev)
-    strides = layout_strides(layers[0])
-    for _ in range(launches):
-        ext.gather_rows(ptrs, s, heads, out.data_ptr(), n, D, BS, strides, 2)
+    if which == "gather":
+        L, NB, BS, H, D = 32, 8192, 16, 8, 128
+        layers = random_cache_layers(L, (2, NB, BS, H, D), torch.bfloat16, dev, seed=0)
+        _, slots = block_table_slots(NB, 1024, BS, seed=2)
+        n = len(slots)
+        ptrs = torch.tensor([t.data_ptr() for t in layers], dtype=torch.long, device=dev)
+        s = torch.from_numpy(slots).to(dev)
+        heads = torch.arange(H, dtype=torch.long, device=dev)
+        out = torch.empty((L, H, n, 2, D), dtype=torch.bfloat16, device=dev)
+        strides = layout_strides(layers[0])
+        for _ in range(launches):
+            ext.gather_rows(ptrs, s, heads, out.data_ptr(), n, D, BS, strides, 2)
+        algo = 2 * L * H * n * 2 * D * 2
+        del layers, out
+    elif which == "scatter":
+        L, NB, BS, H, D = 32, 16384, 16, 8, 128
+        n = NB * BS
+        # the counters count bytes, whatever they hold: the rows are left uninitialised
+        rows = torch.empty((L, H, n, 2, D), device=dev, dtype=torch.bfloat16)
+        caches = [torch.zeros((2, NB, BS, H, D), dtype=torch.bfloat16, device=dev)
+                  for _ in range(L)]
+        _, slots = block_table_slots(NB, NB, BS, seed=4)
+        ptrs = torch.tensor([t.data_ptr() for t in caches], dtype=torch.long, device=dev)
+        s = torch.from_numpy(slots).to(dev)
+        heads = torch.arange(H, dtype=torch.long, device=dev)
+        strides = layout_strides(caches[0])
+        for _ in range(launches):
+            ext.scatter_rows(ptrs, s, heads, rows.data_ptr(), n, D, BS, strides, 2)
+        algo = 2 * L * H * n * 2 * D * 2
+        del rows, caches
+    elif which == "reduce":
+        K, N, SETS = 8, 256 * 8192, 8
+        sets = []
+        for i in range(SETS):
+            bufs = [torch.randn(N, device=dev).to(torch.bfloat16) for _ in range(K)]
+            table = torch.tensor([t.data_ptr() for t in bufs], dtype=torch.long, device=dev)
+            sets.append((bufs, table, torch.empty(N, dtype=torch.bfloat16, device=dev)))
+        flags = torch.ones(8, dtype=torch.long, device=dev)
+        order = torch.tensor([K, *range(K)], dtype=torch.int32, device=dev)
+        state = torch.zeros(REDUCE_STATE_WORDS, dtype=torch.long, device=dev)
+        for i in range(launches):
+            _, table, out = sets[i % SETS]
+            ext.local_reduce(table, flags, order, out, 1, 10**9, 0, state)
+        algo = (K + 1) * N * 2
+        del sets
+    else:
+        raise ValueError(f"no counter workload {which!r}")
     torch.cuda.synchronize()
-    del layers, out
+    torch.cuda.empty_cache()
     a = torch.randn(GIB // 2, device=dev, dtype=torch.float32).to(torch.bfloat16)
     b = torch.empty_like(a)
     for _ in range(launches):
         torch.neg(a, out=b)
     torch.cuda.synchronize()
-    print(f"pmc workload done: {launches} gathers of {2 * L * H * n * 2 * D * 2} algorithmic "
-          f"bytes, {launches} copies of {GIB} bytes", flush=True)
+    print(f"pmc workload done: {launches} {which} calls of {algo} algorithmic bytes, "
+          f"{launches} copies of {GIB} bytes", flush=True)
 
 
 # ------------------------------------------------------------------------------ main
@@ -701,8 +745,10 @@ def main(argv=None):
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--legs", default="",
                     help="comma-separated extra legs to run (default: all; --quick: none)")
-    ap.add_argument("--pmc", action="store_true",
-                    help="only the counter runs' workload (5 gathers, 5 calibration copies)")
+    ap.add_argument("--pmc", nargs="?", const="gather", default=None,
+                    choices=("gather", "scatter", "reduce"),
+                    help="only a counter run's workload: 5 calls of the named kernel (default "
+                         "gather), then 5 calibration copies")
     a = ap.parse_args(argv)
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for "
@@ -716,7 +762,7 @@ def main(argv=None):
     ext = kernels.load()
     torch.cuda.set_device(0)
     if a.pmc:
-        pmc_workload(ext)
+        pmc_workload(ext, a.pmc)
         return 0
     log(f"device {torch.cuda.get_device_name(0)}; library {ext.__file__}")
 
