@@ -45,10 +45,9 @@ HANDLE_BYTES = 64
 _PACKAGE = Path(__file__).resolve().parent
 
 EVS_OK = 0
-
-
 REDUCE_STATE_WORDS = 288
 """64-bit words of local_reduce's state record (EVS_REDUCE_STATE_WORDS in the C header)."""
+
 
 class KernelsUnavailable(RuntimeError):
     """The kernels cannot be loaded here, and why: a wrong or stale build, no GPU."""
@@ -206,6 +205,13 @@ def _device_ptr(t, what: str, dtype) -> int:
     return t.data_ptr()
 
 
+def _one_device(what: str, *tensors) -> None:
+    """The tensors a launch reads must all be on one GPU: the kernel runs there."""
+    devices = {t.device for t in tensors if t is not None}
+    if len(devices) > 1:
+        raise RuntimeError(f"{what}: tensors on several devices ({sorted(map(str, devices))})")
+
+
 class Kernels:
     """The loaded library under the reference module's names (core/csrc/kernels.cpp:9-31).
 
@@ -249,6 +255,7 @@ class Kernels:
         lp = _device_ptr(layer_ptrs, "gather_rows: layer_ptrs", torch.long)
         sp = _device_ptr(slots, "gather_rows: slots", torch.long)
         hp = _device_ptr(heads, "gather_rows: heads", torch.long)
+        _one_device("gather_rows", layer_ptrs, slots, heads)
         st = (ctypes.c_int64 * 5)(*[int(s) for s in strides])
         with torch.cuda.device(slots.device):
             self._check(
@@ -289,6 +296,7 @@ class Kernels:
             so = _device_ptr(slots_out, "gather_blocks: slots_out", torch.long)
             if slots_out.numel() < block_ids.numel() * block_size:
                 raise RuntimeError("gather_blocks: slots_out holds fewer than blocks * block_size")
+        _one_device("gather_blocks", layer_ptrs, block_ids, heads, slots_out)
         st = (ctypes.c_int64 * 5)(*[int(s) for s in strides])
         with torch.cuda.device(block_ids.device):
             self._check(
@@ -323,6 +331,7 @@ class Kernels:
         lp = _device_ptr(layer_ptrs, "scatter_rows: layer_ptrs", torch.long)
         sp = _device_ptr(slots, "scatter_rows: slots", torch.long)
         hp = _device_ptr(heads, "scatter_rows: heads", torch.long)
+        _one_device("scatter_rows", layer_ptrs, slots, heads)
         st = (ctypes.c_int64 * 5)(*[int(s) for s in strides])
         with torch.cuda.device(slots.device):
             self._check(
@@ -395,6 +404,8 @@ class Kernels:
                 or not state.is_contiguous()):
             raise RuntimeError(f"local_reduce: state is {REDUCE_STATE_WORDS} contiguous 64-bit "
                                f"words on the device")
+        _one_device("local_reduce", bufs, None if isinstance(flags, int) else flags, order, out,
+                    state)
         with torch.cuda.device(out.device):
             self._check(
                 self._lib.evs_local_reduce(
@@ -429,13 +440,15 @@ class Kernels:
             raise RuntimeError(f"slot_all_reduce: the order is int32 [count, rows...] of "
                                f"{1 + self.MAX_ROWS}")
         bp = _device_ptr(bufs, "slot_all_reduce: bufs", torch.long)
+        op = _device_ptr(order, "slot_all_reduce: order", torch.int32)
         if seqs.dtype != torch.long or not seqs.is_contiguous():
             raise RuntimeError("slot_all_reduce: seqs are contiguous int64")
+        _one_device("slot_all_reduce", inp, out, bufs, order, seqs)
         with torch.cuda.device(inp.device):
             self._check(
                 self._lib.evs_slot_all_reduce(
                     inp.data_ptr(), out.data_ptr(), inp.numel(), bp, int(ctrl_ptr),
-                    order.data_ptr(), seqs.data_ptr(), seqs.numel(), int(row), int(maxn),
+                    op, seqs.data_ptr(), seqs.numel(), int(row), int(maxn),
                     int(words), 1 if push else 0, int(self.slot_timeout_ns),
                     _stream_of(inp.device),
                 )
