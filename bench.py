@@ -229,6 +229,43 @@ def cpu_baselines_more(seconds=5.0):
     return out
 
 
+# ------------------------------------------------------------------------------ C2 per layout
+def bench_c2_layouts(ext, steps, warmup):
+    """The C2 gather and scatter in each of the three paged layouts (kvcopy.py:37-72), the same
+    1024 blocks; the median of 3 rounds of ``steps`` launches each."""
+    import torch
+
+    L, NB, BS, H, D = 32, 8192, 16, 8, 128
+    dev = torch.device("cuda", 0)
+    stream = torch.cuda.current_stream(dev)
+    shapes = {"kv_first": (2, NB, BS, H, D), "blocks_first": (NB, 2, BS, H, D),
+              "combined": (NB, H, BS, 2 * D)}
+    _, slots = block_table_slots(NB, 1024, BS, seed=2)
+    n = len(slots)
+    s = torch.from_numpy(slots).to(dev)
+    heads = torch.arange(H, dtype=torch.long, device=dev)
+    rows = torch.empty((L, H, n, 2, D), dtype=torch.bfloat16, device=dev)
+    algo = 2 * L * H * n * 2 * D * 2
+    out = {}
+    for name, shape in shapes.items():
+        layers = [torch.empty(shape, dtype=torch.bfloat16, device=dev).normal_() for _ in range(L)]
+        ptrs = torch.tensor([t.data_ptr() for t in layers], dtype=torch.long, device=dev)
+        strides = layout_strides(layers[0])
+        g, w = [], []
+        for _ in range(3):
+            per, _ = time_launches(lambda: ext.gather_rows(ptrs, s, heads, rows.data_ptr(), n, D,
+                                                           BS, strides, 2), steps, warmup, stream)
+            g.append(algo / (sum(per) / len(per)) / 1e6)
+            per, _ = time_launches(lambda: ext.scatter_rows(ptrs, s, heads, rows.data_ptr(), n, D,
+                                                            BS, strides, 2), steps, warmup, stream)
+            w.append(algo / (sum(per) / len(per)) / 1e6)
+        out[name] = {"strides": list(strides), "gather_gbs": round(sorted(g)[1], 1),
+                     "scatter_gbs": round(sorted(w)[1], 1)}
+        del layers
+        torch.cuda.empty_cache()
+    return out
+
+
 # ------------------------------------------------------------------------------ C3 fp8 + D2H
 def bench_c3(ext, steps, warmup):
     import torch
@@ -809,7 +846,8 @@ def main(argv=None):
         result["extra"]["c2_gather_blocks"] = {
             "ms": round(bms, 4), "gbs": round(c2["algo_bytes"] / bms / 1e6, 1),
             "rows_equal_gather_rows": c2["blocks_equal"]}
-    legs = (("c3_fp8_gather_d2h", bench_c3), ("c4_restore", bench_c4),
+    legs = (("c2_layouts", bench_c2_layouts), ("c3_fp8_gather_d2h", bench_c3),
+            ("c4_restore", bench_c4),
             ("restore_host_path", bench_restore_host), ("c5_reduce", bench_c5),
             ("slot_all_reduce", bench_slot), ("decode_overhead", bench_decode_overhead))
     wanted = {x for x in a.legs.split(",") if x}
