@@ -73,3 +73,40 @@ def test_an_incremental_restore_copies_only_the_later_slots(ext):
         oracle.gather_rows(cpu, [9, 10], [0, 1], 2, d, bs, strides_of(cpu[0]), 2),
         oracle.gather_rows(src, [9, 10], [0, 1], 2, d, bs, strides_of(src[0]), 2))
     assert not oracle.gather_rows(cpu, [0, 1, 2, 3], [0, 1], 4, d, bs, strides_of(cpu[0]), 2).any()
+
+
+def test_tables_opened_from_files_and_heads_not_mapped_are_skipped(ext, tmp_path):
+    nb, bs, h, d = 24, 4, 3, 8
+    src = caches("combined", d, torch.bfloat16, n_layers=2, nb=nb, bs=bs, h=h, seed=51)
+    slots = [7, 8, 9, 40, 41, 95]
+    tables, written = commit(src, slots, [0, 1, 2], cap=8)
+    opened = []
+    for t, rows in tables.items():
+        path = tmp_path / f"table{t}.rows"
+        rows.tofile(path)
+        opened.append(Table.open(t, str(path), oracle.written_ranges(written[t])))
+    dst = [torch.zeros_like(t).cuda() for t in src]
+    moves = {0: 2, 2: 1}  # head slot 1's tables are not this rank's: skipped
+    got_rows = Restorer(ext, dst, chunk_bytes=3 * 32).restore(opened, moves)
+    assert got_rows == len(slots) * len(src) * len(moves)
+    cpu = [t.cpu() for t in dst]
+    for theirs, ours in moves.items():
+        assert np.array_equal(
+            oracle.gather_rows(cpu, slots, [ours], 8, d, bs, strides_of(cpu[0]), 2),
+            oracle.gather_rows(src, slots, [theirs], 8, d, bs, strides_of(src[0]), 2))
+    assert not oracle.gather_rows(cpu, list(range(nb * bs)), [0], nb * bs, d, bs,
+                                  strides_of(cpu[0]), 2).any()
+
+
+def test_ranges_outside_a_table_and_partial_rows_are_refused(ext):
+    src = caches("kv_first", 8, torch.bfloat16, n_layers=1, nb=8, bs=4, h=2, seed=61)
+    dst = [torch.zeros_like(t).cuda() for t in src]
+    r = Restorer(ext, dst)
+    rows = np.zeros(32 * 32, dtype=np.uint8)  # 32 slots of 32-byte rows
+    with pytest.raises(ValueError, match="outside"):
+        r.restore([Table(0, rows, [(30, 3)])], {0: 0})
+    with pytest.raises(ValueError, match="outside"):
+        r.restore([Table(1, rows, [(-1, 2)])], {1: 1})
+    with pytest.raises(ValueError, match="whole number"):
+        r.restore([Table(0, rows[:-5], [(0, 1)])], {0: 0})
+    assert not dst[0].any()
