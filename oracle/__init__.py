@@ -34,6 +34,11 @@ expand_blocks                                                          cases
 reduce_protocol            core/csrc/slot.cu:29-40,138-214             the abort/late invariants of
                                                                        core/tests/test_slot_kernel.py
                                                                        :196-224
+float_to_bf16,             c10's float -> bfloat16 rule                torch's own conversion on
+bf16_to_float                                                          edge cases and random values
+cpu_path.*                 core/everserve/state/kvcopy.py:74-128,      equal to the C restatement
+                           core/everserve/state/mirror.py:552-562,     byte for byte (gather,
+                           926-937, reference/arith/ops.py:63-73       restore, member_sum)
 =========================  ==========================================  =============================
 """
 

@@ -166,3 +166,14 @@ def test_the_protocol_sums_zeros_for_missing_members_and_names_them():
     assert (reason, late) == (oracle.REDUCE_DONE, 0)
     out, reason, late = oracle.reduce_protocol(xs, {0: 5}, [0, 1], 5, abort=True)
     assert (reason, late) == (oracle.REDUCE_ABORTED, 1 << 1)
+
+
+@pytest.mark.parametrize("n", [16384, 3000, 2])
+def test_the_cpu_path_member_sum_is_the_oracles(n):
+    """oracle/cpu_path.member_sum is the reduce that bench.py times as the CPU baseline: it must
+    be the same arithmetic, bit for bit, as the checker."""
+    from oracle import cpu_path
+
+    xs = [member_input(r, n) for r in range(8)]
+    got = bf16_bits(cpu_path.member_sum(xs))
+    assert np.array_equal(got, oracle.member_sum([bf16_bits(x) for x in xs]))
