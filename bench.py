@@ -266,6 +266,45 @@ def bench_c2_layouts(ext, steps, warmup):
     return out
 
 
+# ------------------------------------------------------------------------------ store commit
+def bench_store_commit(ext, steps, warmup):
+    """The store's commit copy (store/src/storage.rs:864-957) of a staged step into tables of the
+    C2 shape, with per-row CRC32C, on the host. It commits the C2 step (16,384 slots) and a decode
+    step (64 slots) into warm tables (pages touched at creation, as the store does), on 1 thread
+    and on 16. The sample is 4 of the 32 layers, 32 tables of [131072, 2, 128] bf16: GB/s does
+    not depend on the table count."""
+    import numpy as np
+
+    from everserve_amd.state import staging
+    from everserve_amd.state.store import StoreTables
+
+    L, NB, BS, H, D = 4, 8192, 16, 8, 128
+    rb = 2 * D * 2
+    _, c2_slots = block_table_slots(NB, 1024, BS, seed=2)
+    out = {"config": "4 of 32 layers: 32 tables of [131072, 2, 128] bf16 (2 GiB), warm; the C2 "
+                     "step and its first 64 slots as a decode step"}
+    for name, slots in (("c2_step", c2_slots), ("decode_step", c2_slots[:64])):
+        n = len(slots)
+        cap = staging.capacity_for(n)
+        stage = np.full(L * H * cap * rb, 7, dtype=np.uint8)  # every page touched
+        desc = staging.describe("s", range(L), range(H), cap, D, 2, slots.tolist(), "bfloat16")
+        store = StoreTables(ext, NB * BS)
+        store.commit(stage, desc, 1)  # creates (and touches) the tables
+        res = {}
+        for threads in (1, 16):
+            store.threads = threads
+            reps = max(1, min(steps, 20 if name == "c2_step" else steps))
+            t0 = time.perf_counter()
+            for k in range(reps):
+                store.commit(stage, desc, 2 + k)
+            el = (time.perf_counter() - t0) / reps
+            res[f"threads_{threads}"] = {"ms": round(el * 1e3, 3),
+                                         "gbs": round(L * H * n * rb / el / 1e9, 2)}
+        out[name] = {"slots": n, "bytes": L * H * n * rb, **res}
+        del store, stage
+    return out
+
+
 # ------------------------------------------------------------------------------ C3 fp8 + D2H
 def bench_c3(ext, steps, warmup):
     import torch
@@ -848,7 +887,8 @@ def main(argv=None):
             "rows_equal_gather_rows": c2["blocks_equal"]}
     legs = (("c2_layouts", bench_c2_layouts), ("c3_fp8_gather_d2h", bench_c3),
             ("c4_restore", bench_c4),
-            ("restore_host_path", bench_restore_host), ("c5_reduce", bench_c5),
+            ("restore_host_path", bench_restore_host), ("store_commit", bench_store_commit),
+            ("c5_reduce", bench_c5),
             ("slot_all_reduce", bench_slot), ("decode_overhead", bench_decode_overhead))
     wanted = {x for x in a.legs.split(",") if x}
     unknown = wanted - {name for name, _ in legs}

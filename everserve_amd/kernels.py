@@ -159,6 +159,10 @@ _SIGNATURES: tuple[tuple[str, object, tuple], ...] = (
     ("evs_memset_async", _I32, (_P, _I64, _P)),
     ("evs_copy_rows_async", _I32, (_P, _P, _I64, _I64, _I64, _P)),
     ("evs_host_gather_ranges", _I32, (_P, _I64, _P, _P, _I64, _P, _I64, _P)),
+    ("evs_store_commit", _I32,
+     (_P, _I64, _P, _I64, _P, _P, _P, _I64, _I64, _P, _I64, ctypes.c_uint64, _I64, _P)),
+    ("evs_crc32c", _I32, (_P, _I64, _P)),
+    ("evs_crc32c_rows", _I32, (_P, _I64, _I64, _P)),
     ("evs_event_create", _I32, (_I32, _P)),
     ("evs_event_destroy", _I32, (_P,)),
     ("evs_event_record", _I32, (_P, _P)),
@@ -373,6 +377,66 @@ class Kernels:
                                              int(max_threads), ctypes.byref(rows))
         )
         return rows.value
+
+    # -------------------------------------------------------------- the store's commit copy
+    def store_commit(self, stage, stage_offsets, tables, written_step, crc, num_slots: int,
+                     row_bytes: int, slots, step: int, max_threads: int = 16) -> int:
+        """Commit one staged step's rows into store tables on host threads; the new slot count.
+
+        ``stage`` is a uint8 numpy array (the staged bytes); ``stage_offsets`` int64 [T], where
+        each table's rows start in it; ``tables``, ``written_step`` and ``crc`` are sequences of
+        T numpy arrays: [num_slots * row_bytes] uint8, [num_slots] uint64, [num_slots] uint32.
+        ``slots`` are the step's slot ids (negative: padding). store/src/storage.rs:864-957.
+        """
+        import numpy as np
+
+        T = len(tables)
+        if not (len(written_step) == len(crc) == len(stage_offsets) == T):
+            raise RuntimeError("store_commit: one offset, table, step array and crc array each")
+        for k in range(T):
+            if (tables[k].dtype != np.uint8 or tables[k].size != num_slots * row_bytes
+                    or written_step[k].dtype != np.uint64 or written_step[k].size != num_slots
+                    or crc[k].dtype != np.uint32 or crc[k].size != num_slots
+                    or not (tables[k].flags.c_contiguous and written_step[k].flags.c_contiguous
+                            and crc[k].flags.c_contiguous)):
+                raise RuntimeError(f"store_commit: table {k}'s arrays do not match "
+                                   f"{num_slots} slots of {row_bytes} bytes")
+        if stage.dtype != np.uint8 or not stage.flags.c_contiguous:
+            raise RuntimeError("store_commit: the stage is contiguous uint8")
+        offs = np.ascontiguousarray(stage_offsets, dtype=np.int64)
+        sl = np.ascontiguousarray(slots, dtype=np.int64)
+        ptrs = (ctypes.c_void_p * max(T, 1))(*[t.ctypes.data for t in tables])
+        steps = (ctypes.c_void_p * max(T, 1))(*[w.ctypes.data for w in written_step])
+        crcs = (ctypes.c_void_p * max(T, 1))(*[c.ctypes.data for c in crc])
+        fresh = ctypes.c_int64()
+        self._check(self._lib.evs_store_commit(
+            stage.ctypes.data, stage.size, offs.ctypes.data, T, ptrs, steps, crcs,
+            int(num_slots), int(row_bytes), sl.ctypes.data, sl.size, int(step) & (2**64 - 1),
+            int(max_threads), ctypes.byref(fresh)))
+        return fresh.value
+
+    def crc32c(self, data) -> int:
+        """CRC32C (Castagnoli) of a bytes-like object or a contiguous numpy array."""
+        import numpy as np
+
+        a = np.frombuffer(data, dtype=np.uint8) if isinstance(data, (bytes, bytearray)) else data
+        a = np.ascontiguousarray(a).view(np.uint8).reshape(-1)
+        out = ctypes.c_uint32()
+        self._check(self._lib.evs_crc32c(a.ctypes.data if a.size else None, a.size,
+                                         ctypes.byref(out)))
+        return out.value
+
+    def crc32c_rows(self, rows, row_bytes: int):
+        """CRC32C of each of the consecutive rows of ``rows`` (a contiguous numpy array)."""
+        import numpy as np
+
+        a = np.ascontiguousarray(rows).view(np.uint8).reshape(-1)
+        if a.size % row_bytes:
+            raise RuntimeError("crc32c_rows: not a whole number of rows")
+        out = np.empty(a.size // row_bytes, dtype=np.uint32)
+        self._check(self._lib.evs_crc32c_rows(a.ctypes.data, int(row_bytes), out.size,
+                                              out.ctypes.data))
+        return out
 
     # -------------------------------------------------------------- the reduction stage
     def local_reduce(self, bufs, flags, order, out, epoch: int, timeout_ns: int, ctrl_ptr: int,

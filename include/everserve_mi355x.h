@@ -188,6 +188,33 @@ int evs_host_gather_ranges(const void* src, int64_t row_bytes, const int64_t* st
                            const int64_t* counts, int64_t nranges, void* dst, int64_t max_threads,
                            int64_t* rows_out);
 
+/* The node store's commit copy (store/src/storage.rs:864-957; copy loop :916-943): the rows of
+ * one staged step into `ntables` store tables, on the host.
+ *   stage              the staged bytes (stage_bytes long); table k's rows start at
+ *                      stage_offsets[k], row t at + t * row_bytes (the StagedStep layout,
+ *                      storage.rs:521-540);
+ *   tables[k]          table k's rows, [num_slots, row_bytes];
+ *   written_step[k]    table k's per-slot step of the last write (uint64 [num_slots]);
+ *   crc[k]             table k's per-slot CRC32C of the row as written (uint32 [num_slots]).
+ * For each slot id slots[t] >= 0, row t goes to table row slots[t]; runs of consecutive slot ids
+ * copy as one memcpy; written_step becomes max(step, 1) and crc the Castagnoli CRC32C of the row
+ * (Layer::mark_written, storage.rs:494-504). Negative ids are padding and are skipped. Every slot
+ * id and offset is checked before anything is written (a slot >= num_slots refuses the call).
+ * Tables are independent and are committed on up to max_threads host threads;
+ * *newly_written (if not NULL) receives the slots written for the first time, over all tables.
+ * Host memory only, no device call. */
+int evs_store_commit(const void* stage, int64_t stage_bytes, const int64_t* stage_offsets,
+                     int64_t ntables, void* const* tables, uint64_t* const* written_step,
+                     uint32_t* const* crc, int64_t num_slots, int64_t row_bytes,
+                     const int64_t* slots, int64_t nslots, uint64_t step, int64_t max_threads,
+                     int64_t* newly_written);
+
+/* CRC32C (Castagnoli: reflected polynomial 0x82F63B78, initial value and final xor 0xFFFFFFFF),
+ * the checksum the store keeps per row (the crc32c crate, store/Cargo.toml:25): of `bytes` bytes
+ * into *out, and of `rows` consecutive rows of row_bytes each into out[0..rows). Host only. */
+int evs_crc32c(const void* data, int64_t bytes, uint32_t* out);
+int evs_crc32c_rows(const void* data, int64_t row_bytes, int64_t rows, uint32_t* out);
+
 /* Stream-to-stream ordering on one device without a cache writeback. A HIP event records with a
  * system-scope fence by default (the L2 written back and invalidated at the record); ordering one
  * stream's later work after another's on the same device needs none of it, since every kernel

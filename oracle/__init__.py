@@ -34,6 +34,9 @@ expand_blocks                                                          cases
 reduce_protocol            core/csrc/slot.cu:29-40,138-214             the abort/late invariants of
                                                                        core/tests/test_slot_kernel.py
                                                                        :196-224
+crc32c, crc32c_rows        the crc32c crate 0.6.8 (store/Cargo.toml:   the published check value and
+                           25), RFC 3720 B.4                           RFC 3720's vectors; the CRC's
+                                                                       affine law on random data
 float_to_bf16,             c10's float -> bfloat16 rule                torch's own conversion on
 bf16_to_float                                                          edge cases and random values
 cpu_path.*                 core/everserve/state/kvcopy.py:74-128,      equal to the C restatement
@@ -271,20 +274,28 @@ def derive(step: Mapping) -> list[tuple[int, int]]:
 
 
 def store_commit(stage_bytes: np.ndarray, step: Mapping, tables: dict[int, np.ndarray],
-                 num_slots: int, written: dict[int, np.ndarray], step_no: int) -> None:
+                 num_slots: int, written: dict[int, np.ndarray], step_no: int,
+                 crcs: dict[int, np.ndarray] | None = None) -> None:
     """Copy the staged rows into per-(layer, head) tables, as the store's commit does.
 
     store/src/storage.rs:864-957 (copy loop 916-943): for each table, runs of consecutive
     non-negative slot ids copy as one memcpy from ``offset + i * row_bytes``; padding (negative)
-    is skipped; each written slot records ``step_no``. Tables are created zeroed on first use as
-    ``num_slots * row_bytes`` bytes.
+    is skipped; each written slot records max(step_no, 1) (Layer::note_written, :498-504) and,
+    when ``crcs`` is given, the CRC32C of its row as it stands after the copy
+    (Layer::mark_written, :494-497). Tables are created zeroed on first use as
+    ``num_slots * row_bytes`` bytes. Every slot id is checked before anything is written.
     """
     row_bytes = step["shape"][0] * step["shape"][1] * DTYPE_BYTES[step["dtype"]]
     slots = step["slots"]
+    for s in slots:
+        if s >= num_slots:
+            raise ValueError(f"slot {s} outside 0..{num_slots}")
     for table, offset in derive(step):
         if table not in tables:
             tables[table] = np.zeros(num_slots * row_bytes, dtype=np.uint8)
             written[table] = np.zeros(num_slots, dtype=np.uint64)
+            if crcs is not None:
+                crcs[table] = np.zeros(num_slots, dtype=np.uint32)
         rows, marks = tables[table], written[table]
         i = 0
         while i < len(slots):
@@ -292,15 +303,53 @@ def store_commit(stage_bytes: np.ndarray, step: Mapping, tables: dict[int, np.nd
             if s < 0:
                 i += 1
                 continue
-            if s >= num_slots:
-                raise ValueError(f"slot {s} outside 0..{num_slots}")
             run = 1
             while i + run < len(slots) and slots[i + run] == s + run:
                 run += 1
             src = offset + i * row_bytes
             rows[s * row_bytes:(s + run) * row_bytes] = stage_bytes[src:src + run * row_bytes]
-            marks[s:s + run] = step_no
+            marks[s:s + run] = max(step_no, 1)
             i += run
+        if crcs is not None:
+            live = np.array(sorted({s for s in slots if s >= 0}), dtype=np.int64)
+            if live.size:
+                crcs[table][live] = crc32c_rows(rows.reshape(num_slots, row_bytes)[live])
+
+
+_CRC32C_TABLE: np.ndarray | None = None
+
+
+def _crc32c_table() -> np.ndarray:
+    """The byte table of the reflected Castagnoli polynomial, built bit by bit."""
+    global _CRC32C_TABLE
+    if _CRC32C_TABLE is None:
+        t = np.zeros(256, dtype=np.uint32)
+        for i in range(256):
+            c = i
+            for _ in range(8):
+                c = (c >> 1) ^ (0x82F63B78 if c & 1 else 0)
+            t[i] = c
+        _CRC32C_TABLE = t
+    return _CRC32C_TABLE
+
+
+def crc32c_rows(rows: np.ndarray) -> np.ndarray:
+    """CRC32C (Castagnoli, RFC 3720 B.4: reflected polynomial 0x82F63B78, initial value and
+    final xor 0xFFFFFFFF) of every row of a [n, row_bytes] uint8 array, one byte of every row at
+    a time. The store keeps one per written row (store/src/storage.rs:371-373, the crc32c crate
+    0.6.8, store/Cargo.toml:25)."""
+    rows = np.ascontiguousarray(rows, dtype=np.uint8)
+    t = _crc32c_table()
+    c = np.full(rows.shape[0], 0xFFFFFFFF, dtype=np.uint32)
+    for j in range(rows.shape[1]):
+        c = t[(c ^ rows[:, j]) & 0xFF] ^ (c >> np.uint32(8))
+    return c ^ np.uint32(0xFFFFFFFF)
+
+
+def crc32c(data) -> int:
+    """CRC32C of one byte string (see crc32c_rows)."""
+    a = np.frombuffer(bytes(data), dtype=np.uint8)
+    return int(crc32c_rows(a.reshape(1, -1))[0])
 
 
 def written_ranges(marks: np.ndarray, since_step: int = 0) -> list[tuple[int, int]]:
