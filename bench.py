@@ -229,6 +229,49 @@ def cpu_baselines_more(seconds=5.0):
     return out
 
 
+# ------------------------------------------------------------------------------ C1
+def bench_c1(ext, steps, warmup):
+    """Config C1 (Qwen2.5-0.5B shape, the reference's CPU-runnable
+    case): 24 layers of [2, 2048, 16, 2, 64] bf16, 128 random blocks, both heads. The gather on the
+    GPU beside the reference's torch CPU path on the same workload (mirror.py:552-562)."""
+    import numpy as np
+    import torch
+
+    from oracle import cpu_path
+
+    L, NB, BS, H, D = 24, 2048, 16, 2, 64
+    dev = torch.device("cuda", 0)
+    stream = torch.cuda.current_stream(dev)
+    g = torch.Generator().manual_seed(0)
+    cpu_layers = [torch.randn((2, NB, BS, H, D), generator=g).to(torch.bfloat16) for _ in range(L)]
+    blocks = np.random.default_rng(1).choice(NB, 128, replace=False)
+    slots = (blocks[:, None] * BS + np.arange(BS)[None, :]).reshape(-1).astype(np.int64)
+    n = len(slots)
+    layers = [t.to(dev) for t in cpu_layers]
+    ptrs = torch.tensor([t.data_ptr() for t in layers], dtype=torch.long, device=dev)
+    s = torch.from_numpy(slots).to(dev)
+    heads = torch.arange(H, dtype=torch.long, device=dev)
+    out = torch.empty((L, H, n, 2, D), dtype=torch.bfloat16, device=dev)
+    strides = layout_strides(layers[0])
+    algo = 2 * L * H * n * 2 * D * 2
+    per, _ = time_launches(lambda: ext.gather_rows(ptrs, s, heads, out.data_ptr(), n, D, BS,
+                                                   strides, 2), steps, warmup, stream)
+    ms = sum(per) / len(per)
+    staged = torch.empty((L, H, n, 2, D), dtype=torch.bfloat16)
+    cs, ch = torch.from_numpy(slots), torch.arange(H)
+    cpu_path.gather_step(cpu_layers, cs, ch, n, out=staged)
+    reps, t0 = 0, time.perf_counter()
+    while reps < 3 or time.perf_counter() - t0 < 2.0:
+        cpu_path.gather_step(cpu_layers, cs, ch, n, out=staged)
+        reps += 1
+    cpu_ms = (time.perf_counter() - t0) / reps * 1e3
+    same = bool(torch.equal(out.cpu().view(torch.int16), staged.view(torch.int16)))
+    return {"config": "C1 Qwen2.5-0.5B: 24 x [2, 2048, 16, 2, 64] bf16, 128 blocks, heads [0, 1]",
+            "bytes": algo, "gpu_ms": round(ms, 4), "gpu_gbs": round(algo / ms / 1e6, 1),
+            "cpu_ms": round(cpu_ms, 3), "cpu_gbs": round(algo / cpu_ms / 1e6, 2),
+            "cpu_threads": torch.get_num_threads(), "rows_equal_cpu_path": same}
+
+
 # ------------------------------------------------------------------------------ C2 per layout
 def bench_c2_layouts(ext, steps, warmup):
     """The C2 gather and scatter in each of the three paged layouts (kvcopy.py:37-72), the same
@@ -885,7 +928,8 @@ def main(argv=None):
         result["extra"]["c2_gather_blocks"] = {
             "ms": round(bms, 4), "gbs": round(c2["algo_bytes"] / bms / 1e6, 1),
             "rows_equal_gather_rows": c2["blocks_equal"]}
-    legs = (("c2_layouts", bench_c2_layouts), ("c3_fp8_gather_d2h", bench_c3),
+    legs = (("c1_gather", bench_c1), ("c2_layouts", bench_c2_layouts),
+            ("c3_fp8_gather_d2h", bench_c3),
             ("c4_restore", bench_c4),
             ("restore_host_path", bench_restore_host), ("store_commit", bench_store_commit),
             ("c5_reduce", bench_c5),
