@@ -598,12 +598,12 @@ def bench_c5(ext, steps, warmup):
 
     from everserve_amd.kernels import REDUCE_STATE_WORDS
 
-    K, N, SETS = 8, 256 * 8192, 8
+    K, N, SETS = 8, 256 * 8192, 32
     dev = torch.device("cuda", 0)
     stream = torch.cuda.current_stream(dev)
     g = torch.Generator(device=dev).manual_seed(5)
     sets = []
-    for _ in range(SETS):  # 8 sets x 36 MiB: more than the 256 MB Infinity Cache holds
+    for _ in range(SETS):  # 32 sets x 36 MiB = 1.1 GiB: over 4x what the Infinity Cache holds
         bufs = [torch.randn(N, generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
                 for _ in range(K)]
         table = torch.tensor([t.data_ptr() for t in bufs], dtype=torch.long, device=dev)
@@ -624,7 +624,7 @@ def bench_c5(ext, steps, warmup):
     eager_out = [out.clone() for _, _, out in sets]
     for _, _, out in sets:
         out.zero_()
-    # the kernel's own cost: the 8 calls captured in a HIP graph (the reduce is capturable: no
+    # the kernel's own cost: the 32 calls captured in a HIP graph (the reduce is capturable: no
     # memset, its counters reset themselves) and replayed, so no host launch sits between calls
     side = torch.cuda.Stream(device=dev)
     graph = torch.cuda.CUDAGraph()
@@ -651,7 +651,7 @@ def bench_c5(ext, steps, warmup):
     algo = (K + 1) * N * 2
     return {
         "config": "C5 local reduce: 8 bf16 buffers of 256 x 8192, fp32 accumulation in order; "
-                  "8 buffer sets rotating (288 MiB, more than the Infinity Cache)",
+                  "32 buffer sets rotating (1.1 GiB, over 4x the 256 MB Infinity Cache)",
         "us_per_call": round(us, 2),
         "us_per_call_eager_launches": round(sum(eager) / len(eager) * 1e3, 2),
         "gbs": round(algo / us / 1e3, 1),
@@ -827,7 +827,7 @@ def pmc_workload(ext, which="gather", launches=5):
         algo = 2 * L * H * n * 2 * D * 2
         del rows, caches
     elif which == "reduce":
-        K, N, SETS = 8, 256 * 8192, 8
+        K, N, SETS = 8, 256 * 8192, 32
         sets = []
         for i in range(SETS):
             bufs = [torch.randn(N, device=dev).to(torch.bfloat16) for _ in range(K)]
