@@ -36,8 +36,12 @@ namespace {
 #ifndef EVS_SCATTER_THREADS
 #define EVS_SCATTER_THREADS 128
 #endif
-#ifndef EVS_ROWS_VPT
-#define EVS_ROWS_VPT 2
+// Words per thread per pass, per direction: all of a pass's loads are issued before its stores.
+#ifndef EVS_GATHER_VPT
+#define EVS_GATHER_VPT 2
+#endif
+#ifndef EVS_SCATTER_VPT
+#define EVS_SCATTER_VPT 2
 #endif
 // Per direction, bit 0: nontemporal loads, bit 1: nontemporal stores. Every byte here is touched
 // once, so no line is worth keeping in L2 or the Infinity Cache.
@@ -86,7 +90,6 @@ constexpr uint32_t kXcds = 8;
 #define EVS_SCATTER_GROUP_FASTEST 0
 #endif
 
-constexpr int kVpt = EVS_ROWS_VPT;  // words per thread per pass, all loads issued before stores
 constexpr int kMaxTileSlots = 64;
 constexpr int kMaxHeads = 256;      // LDS table of head offsets
 
@@ -95,14 +98,18 @@ enum Dir : int { kGather = 0, kScatter = 1 };
 constexpr int threads_of(int d) { return d == kGather ? EVS_GATHER_THREADS : EVS_SCATTER_THREADS; }
 constexpr int nt_of(int d) { return d == kGather ? EVS_GATHER_NT : EVS_SCATTER_NT; }
 constexpr int order_of(int d) { return d == kGather ? EVS_GATHER_ORDER : EVS_SCATTER_ORDER; }
+constexpr int vpt_of(int d) { return d == kGather ? EVS_GATHER_VPT : EVS_SCATTER_VPT; }
 static_assert(threads_of(kGather) >= kMaxTileSlots && threads_of(kScatter) >= kMaxTileSlots,
               "the first TS threads fill a tile's slot offsets: a workgroup needs kMaxTileSlots");
 enum Index : int { kBySlots = 0, kByBlocks = 1 };
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kSinkWords = 256 * kVpt;  // one word per thread and pass, at the widest workgroup
-static_assert(threads_of(kGather) <= 256 && threads_of(kScatter) <= 256, "the sink holds 256 threads");
+// one cell per word of a pass, at the widest pass
+constexpr int kSinkWords = 1024;
+static_assert(threads_of(kGather) * vpt_of(kGather) <= kSinkWords &&
+                  threads_of(kScatter) * vpt_of(kScatter) <= kSinkWords,
+              "the sink holds one cell per word of a pass");
 
 // Where a gathered word that moves nothing goes: a lane with no word (a slot past n, a word past
 // the tile) loads from and stores into its own 16-byte cell here instead of branching around the
@@ -281,6 +288,7 @@ __device__ __forceinline__ void move_tile(const RowsArgs& a, const int64_t* s_sl
 
   constexpr int kThreads = threads_of(D);
   char* sink = reinterpret_cast<char*>(g_sink) + tid * sizeof(u32x4);
+  constexpr int kVpt = vpt_of(D);
   for (uint32_t v0 = 0; v0 < a.tile_words; v0 += kThreads * kVpt) {
     T w[kVpt];
     const char* src[kVpt];
