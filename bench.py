@@ -95,6 +95,27 @@ def time_launches(fn, steps, warmup, stream):
     return per, wall
 
 
+def pinned_copy_gbs(nbytes, to_host, repeats=5):
+    """GB/s of a plain copy between pinned host memory and HBM (torch's copy of a contiguous
+    tensor, one hipMemcpyAsync): the measured ceiling the PCIe-bound copies are set against."""
+    import torch
+
+    dev = torch.device("cuda", 0)
+    d = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    h = torch.empty(nbytes, dtype=torch.uint8, pin_memory=True)
+
+    def copy():
+        if to_host:
+            h.copy_(d, non_blocking=True)
+        else:
+            d.copy_(h, non_blocking=True)
+
+    per, _ = time_launches(copy, repeats, 1, torch.cuda.current_stream(dev))
+    torch.cuda.synchronize()
+    del d, h
+    return nbytes / (sum(per) / len(per)) / 1e6
+
+
 def pmc_traffic():
     """HBM bytes per launch from the committed rocprofv3 counter profile, or None."""
     if not PMC_PROFILE.is_file():
@@ -391,6 +412,7 @@ def bench_c3(ext, steps, warmup):
                           staging[7, 0, :BS].view(-1).cpu()))
     del layers, staging
     torch.cuda.empty_cache()
+    plain = pinned_copy_gbs(payload, to_host=True)
     g_ms, c_ms, b_ms = (sum(x) / len(x) for x in (g_per, c_per, b_per))
     return {
         "config": "C3 Llama-3-70B one-rank share, fp8 e4m3 [2,8192,16,1,128] x 80, 2048 blocks",
@@ -401,6 +423,8 @@ def bench_c3(ext, steps, warmup):
         "d2h_ms": round(c_ms, 3),
         "d2h_pcie_gbs": round(payload / c_ms / 1e6, 2),
         "d2h_frac_of_64gbs": round(payload / c_ms / 1e6 / 64.0, 4),
+        "d2h_plain_memcpy_gbs": round(plain, 2),
+        "d2h_frac_of_plain_memcpy": round(payload / c_ms / 1e6 / plain, 4),
         "gather_plus_d2h_ms": round(b_ms, 3),
         "scales": "80 fp32 per-layer scales copied beside the rows (not inside them)",
         "bytes_equal_after_d2h": ok,
@@ -511,6 +535,7 @@ def bench_restore_host(ext, steps, warmup):
         shutil.rmtree(tmp, ignore_errors=True)
     del caches
     torch.cuda.empty_cache()
+    plain = pinned_copy_gbs(1 << 30, to_host=False)
     return {
         "config": f"restore of {L * H} store tables of C4 shape ([262144, 2, 128] bf16, 128 MiB "
                   f"each, every slot written) from /dev/shm files into a fresh 16384-block cache "
@@ -521,6 +546,8 @@ def bench_restore_host(ext, steps, warmup):
         "reference_procedure_s": round(ref_s, 3),
         "reference_procedure_gbs": round(payload / ref_s / 1e9, 2),
         "speedup": round(ref_s / ours_s, 2),
+        "h2d_plain_memcpy_gbs": round(plain, 2),
+        "frac_of_plain_h2d": round(payload / ours_s / 1e9 / plain, 4),
         "rows_check": ok,
         "host_threads": restorer._threads,
     }
