@@ -54,16 +54,8 @@ def random_cache_layers(n_layers, shape, dtype, device, seed):
     import torch
 
     g = torch.Generator(device=device).manual_seed(seed)
-    layers = []
-    for _ in range(n_layers):
-        t = torch.empty(shape, dtype=dtype, device=device)
-        if dtype in (torch.float8_e4m3fn, torch.float8_e5m2):
-            layers.append(torch.randn(shape, generator=g, device=device, dtype=torch.float16)
-                          .clamp_(-448, 448).to(dtype))
-        else:
-            t.normal_(generator=g)
-            layers.append(t)
-    return layers
+    return [torch.empty(shape, dtype=dtype, device=device).normal_(generator=g)
+            for _ in range(n_layers)]
 
 
 def block_table_slots(num_blocks_cache, num_blocks, block_size, seed):
@@ -373,12 +365,16 @@ def bench_store_commit(ext, steps, warmup):
 def bench_c3(ext, steps, warmup):
     import torch
 
+    import numpy as np
+
     L, NB, BS, H, D = 80, 8192, 16, 1, 128
     dev = torch.device("cuda", 0)
     stream = torch.cuda.current_stream(dev)
-    layers = random_cache_layers(L, (2, NB, BS, H, D), torch.float8_e4m3fn, dev, seed=3)
-    scales = torch.empty(L, dtype=torch.float32).uniform_(0.01, 0.1,
-                                                          generator=torch.Generator().manual_seed(3))
+    # per-layer scales s_l ~ U(0.01, 0.1) and values fp8(N(0,1) / s_l), clamped to e4m3's range
+    scales = torch.from_numpy(np.random.default_rng(3).uniform(0.01, 0.1, L).astype(np.float32))
+    g = torch.Generator(device=dev).manual_seed(3)
+    layers = [(torch.randn((2, NB, BS, H, D), generator=g, device=dev, dtype=torch.float16)
+               / float(sl)).clamp_(-448, 448).to(torch.float8_e4m3fn) for sl in scales.tolist()]
     _, slots = block_table_slots(NB, 2048, BS, seed=3)
     n = len(slots)
     ptrs = torch.tensor([t.data_ptr() for t in layers], dtype=torch.long, device=dev)
@@ -426,7 +422,8 @@ def bench_c3(ext, steps, warmup):
         "d2h_plain_memcpy_gbs": round(plain, 2),
         "d2h_frac_of_plain_memcpy": round(payload / c_ms / 1e6 / plain, 4),
         "gather_plus_d2h_ms": round(b_ms, 3),
-        "scales": "80 fp32 per-layer scales copied beside the rows (not inside them)",
+        "scales": "80 fp32 per-layer scales U(0.01, 0.1) copied beside the rows (not inside "
+                  "them); values fp8(N(0,1) / scale)",
         "bytes_equal_after_d2h": ok,
     }
 
@@ -628,11 +625,12 @@ def bench_c5(ext, steps, warmup):
     K, N, SETS = 8, 256 * 8192, 32
     dev = torch.device("cuda", 0)
     stream = torch.cuda.current_stream(dev)
-    g = torch.Generator(device=dev).manual_seed(5)
     sets = []
-    for _ in range(SETS):  # 32 sets x 36 MiB = 1.1 GiB: over 4x what the Infinity Cache holds
-        bufs = [torch.randn(N, generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
-                for _ in range(K)]
+    for j in range(SETS):  # 32 sets x 36 MiB = 1.1 GiB: over 4x what the Infinity Cache holds
+        # buffer i of set j from manual_seed(5 + i + 8 j): set 0 is the config's 5 + i
+        bufs = [torch.randn(N, generator=torch.Generator(device=dev).manual_seed(5 + i + K * j),
+                            device=dev, dtype=torch.float32).to(torch.bfloat16)
+                for i in range(K)]
         table = torch.tensor([t.data_ptr() for t in bufs], dtype=torch.long, device=dev)
         out = torch.empty(N, dtype=torch.bfloat16, device=dev)
         sets.append((bufs, table, out))
