@@ -70,6 +70,33 @@ namespace {
 #define EVS_SCATTER_XCD_CHUNK 64
 #endif
 constexpr uint32_t kXcds = 8;
+// The pair scatter (a staged row per listed slot, listed in the order the caller wants written):
+// its tiles span all heads (2 slots x 8 heads at bf16 d=128, 8 KiB) and its words run along the
+// cache, so that a caller listing its slots in increasing order writes each layer's cache front
+// to back. A tile is one pass (256 threads x 2 words) and its reads, which are random, are
+// nontemporal, as the gather's are. On C4's permuted block table with the pairs in slot order it
+// measured 5,994 GB/s, against 5,660 for the scatter in staged order on the same box.
+#ifndef EVS_PAIRS_TILE_WORDS
+#define EVS_PAIRS_TILE_WORDS 512
+#endif
+#ifndef EVS_PAIRS_HEADS_PER_TILE
+#define EVS_PAIRS_HEADS_PER_TILE 0
+#endif
+#ifndef EVS_PAIRS_ORDER
+#define EVS_PAIRS_ORDER 0
+#endif
+#ifndef EVS_PAIRS_XCD_CHUNK
+#define EVS_PAIRS_XCD_CHUNK 64
+#endif
+#ifndef EVS_PAIRS_THREADS
+#define EVS_PAIRS_THREADS 256
+#endif
+#ifndef EVS_PAIRS_NT
+#define EVS_PAIRS_NT 3  // its reads are random, as the gather's are: nontemporal both ways
+#endif
+#ifndef EVS_PAIRS_VPT
+#define EVS_PAIRS_VPT 2
+#endif
 // Tile shape per direction: words a tile aims at, heads it covers (0: all), head groups fastest.
 #ifndef EVS_GATHER_TILE_WORDS
 #define EVS_GATHER_TILE_WORDS 512
@@ -94,21 +121,34 @@ constexpr int kMaxTileSlots = 64;
 constexpr int kMaxHeads = 256;      // LDS table of head offsets
 
 enum Dir : int { kGather = 0, kScatter = 1 };
+// kBySlots: row t of a layer's staging goes to (or comes from) slot slots[t]; kByBlocks: row t is
+// offset t % bs of the (t / bs)-th listed block; kByPairs (scatter): staged row rows_of[i] goes
+// to slot slots[i].
+enum Index : int { kBySlots = 0, kByBlocks = 1, kByPairs = 2 };
 
-constexpr int threads_of(int d) { return d == kGather ? EVS_GATHER_THREADS : EVS_SCATTER_THREADS; }
-constexpr int nt_of(int d) { return d == kGather ? EVS_GATHER_NT : EVS_SCATTER_NT; }
+constexpr int threads_of(int d, int i) {
+  return i == kByPairs ? EVS_PAIRS_THREADS : d == kGather ? EVS_GATHER_THREADS : EVS_SCATTER_THREADS;
+}
+constexpr int vpt_of(int d, int i) {
+  return i == kByPairs ? EVS_PAIRS_VPT : d == kGather ? EVS_GATHER_VPT : EVS_SCATTER_VPT;
+}
+constexpr int nt_of(int d, int i) {
+  return i == kByPairs ? EVS_PAIRS_NT : d == kGather ? EVS_GATHER_NT : EVS_SCATTER_NT;
+}
 constexpr int order_of(int d) { return d == kGather ? EVS_GATHER_ORDER : EVS_SCATTER_ORDER; }
-constexpr int vpt_of(int d) { return d == kGather ? EVS_GATHER_VPT : EVS_SCATTER_VPT; }
-static_assert(threads_of(kGather) >= kMaxTileSlots && threads_of(kScatter) >= kMaxTileSlots,
+constexpr int word_order(int d, int i) { return i == kByPairs ? EVS_PAIRS_ORDER : order_of(d); }
+static_assert(threads_of(kGather, kBySlots) >= kMaxTileSlots &&
+                  threads_of(kScatter, kBySlots) >= kMaxTileSlots &&
+                  threads_of(kScatter, kByPairs) >= kMaxTileSlots,
               "the first TS threads fill a tile's slot offsets: a workgroup needs kMaxTileSlots");
-enum Index : int { kBySlots = 0, kByBlocks = 1 };
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // one cell per word of a pass, at the widest pass
 constexpr int kSinkWords = 1024;
-static_assert(threads_of(kGather) * vpt_of(kGather) <= kSinkWords &&
-                  threads_of(kScatter) * vpt_of(kScatter) <= kSinkWords,
+static_assert(threads_of(kGather, kBySlots) * vpt_of(kGather, kBySlots) <= kSinkWords &&
+                  threads_of(kScatter, kBySlots) * vpt_of(kScatter, kBySlots) <= kSinkWords &&
+                  threads_of(kScatter, kByPairs) * vpt_of(kScatter, kByPairs) <= kSinkWords,
               "the sink holds one cell per word of a pass");
 
 // Where a gathered word that moves nothing goes: a lane with no word (a slot past n, a word past
@@ -127,6 +167,7 @@ struct RowsArgs {
   const int64_t* heads;       // device head slots
   char* rows;                 // the staging buffer, [L, H, cap, 2, d]
   int64_t* slots_out;         // kByBlocks: the expanded slot ids, or null
+  const int64_t* rows_of;     // kByPairs: the staged row of each listed slot
   int64_t n;                  // slots moved per layer
   int64_t cap;                // staging capacity (rows per (layer, head))
   int64_t half_bytes;         // d * elem
@@ -252,12 +293,12 @@ struct WordAt {
   uint32_t h, tl, k, j;
 };
 
-template <int D>
+template <int kOrder>
 __device__ __forceinline__ WordAt word_at(const RowsArgs& a, uint32_t v) {
   WordAt w;
   uint32_t q, q2;
   a.div_w.divmod(v, q, w.j);
-  if (order_of(D) == 0) {
+  if (kOrder == 0) {
     // v = ((k * TS + tl) * HG + h) * W + j
     a.div_h.divmod(q, q2, w.h);
     a.div_ts.divmod(q2, w.k, w.tl);
@@ -269,26 +310,28 @@ __device__ __forceinline__ WordAt word_at(const RowsArgs& a, uint32_t v) {
   return w;
 }
 
-// Byte offset of a word in the layer's part of the staging buffer.
-__device__ __forceinline__ int64_t staged_offset(const RowsArgs& a, uint32_t h0, int64_t t0,
+// Byte offset of a word of staged row `row` in the layer's part of the staging buffer.
+__device__ __forceinline__ int64_t staged_offset(const RowsArgs& a, uint32_t h0, int64_t row,
                                                  const WordAt& w, int64_t word_bytes) {
-  return (static_cast<int64_t>(h0 + w.h) * a.cap + t0 + w.tl) * (2 * a.half_bytes) +
+  return (static_cast<int64_t>(h0 + w.h) * a.cap + row) * (2 * a.half_bytes) +
          w.k * a.half_bytes + static_cast<int64_t>(w.j) * word_bytes;
 }
 
-// Move one tile's words: the slots' offsets and the heads' are in LDS.
-template <typename T, int D>
+// Move one tile's words: the slots' offsets and the heads' are in LDS, and for the pair scatter
+// the staged rows'.
+template <typename T, int D, int I>
 __device__ __forceinline__ void move_tile(const RowsArgs& a, const int64_t* s_slot,
-                                          const int64_t* s_head, int64_t layer_base,
-                                          uint32_t layer, uint32_t group, int64_t t0) {
+                                          const int64_t* s_head, const int64_t* s_src,
+                                          int64_t layer_base, uint32_t layer, uint32_t group,
+                                          int64_t t0) {
   const uint32_t h0 = group * a.HG;
   const int tid = threadIdx.x;
   char* cache_w = reinterpret_cast<char*>(layer_base);
   char* rows_l = a.rows + static_cast<int64_t>(layer) * a.H * a.cap * (2 * a.half_bytes);
 
-  constexpr int kThreads = threads_of(D);
+  constexpr int kThreads = threads_of(D, I);
   char* sink = reinterpret_cast<char*>(g_sink) + tid * sizeof(u32x4);
-  constexpr int kVpt = vpt_of(D);
+  constexpr int kVpt = vpt_of(D, I);
   for (uint32_t v0 = 0; v0 < a.tile_words; v0 += kThreads * kVpt) {
     T w[kVpt];
     const char* src[kVpt];
@@ -297,11 +340,12 @@ __device__ __forceinline__ void move_tile(const RowsArgs& a, const int64_t* s_sl
 #pragma unroll
     for (int i = 0; i < kVpt; i++) {
       const uint32_t v = v0 + i * kThreads + tid;
-      const WordAt at = word_at<D>(a, v);
+      const WordAt at = word_at<word_order(D, I)>(a, v);
       const bool in_tile = v < a.tile_words && h0 + at.h < static_cast<uint32_t>(a.H);
       const int64_t slot_off = in_tile ? s_slot[at.tl] : -1;
       char* cache = cache_w + slot_off + s_head[in_tile ? at.h : 0] + at.k * a.skv + at.j * a.sj;
-      char* staged = rows_l + staged_offset(a, h0, t0, at, sizeof(T));
+      const int64_t row = I == kByPairs ? s_src[at.tl] : t0 + at.tl;
+      char* staged = rows_l + staged_offset(a, h0, row, at, sizeof(T));
       char* cell = sink + i * kThreads * sizeof(u32x4);
       live[i] = slot_off >= 0;
       src[i] = live[i] ? (D == kGather ? cache : staged) : cell;
@@ -309,16 +353,16 @@ __device__ __forceinline__ void move_tile(const RowsArgs& a, const int64_t* s_sl
     }
     if (D == kGather) {
 #pragma unroll
-      for (int i = 0; i < kVpt; i++) w[i] = load_word<T, (nt_of(D) & 1) != 0>(src[i]);
+      for (int i = 0; i < kVpt; i++) w[i] = load_word<T, (nt_of(D, I) & 1) != 0>(src[i]);
 #pragma unroll
-      for (int i = 0; i < kVpt; i++) store_word<T, (nt_of(D) & 2) != 0>(dst[i], w[i]);
+      for (int i = 0; i < kVpt; i++) store_word<T, (nt_of(D, I) & 2) != 0>(dst[i], w[i]);
     } else {
 #pragma unroll
       for (int i = 0; i < kVpt; i++)
-        if (live[i]) w[i] = load_word<T, (nt_of(D) & 1) != 0>(src[i]);
+        if (live[i]) w[i] = load_word<T, (nt_of(D, I) & 1) != 0>(src[i]);
 #pragma unroll
       for (int i = 0; i < kVpt; i++)
-        if (live[i]) store_word<T, (nt_of(D) & 2) != 0>(dst[i], w[i]);
+        if (live[i]) store_word<T, (nt_of(D, I) & 2) != 0>(dst[i], w[i]);
     }
   }
 }
@@ -328,25 +372,35 @@ __device__ __forceinline__ void move_tile(const RowsArgs& a, const int64_t* s_sl
 // heads read the tile's last entry again, so that the reads touch only the tile's own lines.
 template <int D, int I>
 __device__ __forceinline__ void tile_offsets(const RowsArgs& a, const TileId& id, int64_t t0,
-                                             int64_t* s_slot, int64_t* s_head) {
+                                             int64_t* s_slot, int64_t* s_head, int64_t* s_src) {
   const int tid = threadIdx.x;
   const int h0 = static_cast<int>(id.group) * a.HG;
   if (tid < kMaxTileSlots) {
-    const int64_t entry = index_entry<I>(a, t0 + (tid < a.TS ? tid : a.TS - 1));
+    const int64_t t = t0 + (tid < a.TS ? tid : a.TS - 1);
+    const int64_t entry = index_entry<I == kByPairs ? kBySlots : I>(a, t);
+    const int64_t src = I == kByPairs ? a.rows_of[t < a.n ? t : a.n - 1] : 0;
     const int hc = h0 + (tid < a.HG ? tid : a.HG - 1);
     const int64_t head = a.heads[hc < a.H ? hc : a.H - 1];
-    if (tid < a.TS) s_slot[tid] = slot_offset<D, I>(a, id.layer, t0 + tid, entry);
+    if (tid < a.TS) {
+      int64_t off = slot_offset<D, I == kByPairs ? kBySlots : I>(a, id.layer, t0 + tid, entry);
+      if (I == kByPairs) {
+        if (src < 0 || src >= a.cap) off = -1;  // a staged row outside the buffer moves nothing
+        s_src[tid] = src;
+      }
+      s_slot[tid] = off;
+    }
     if (tid < a.HG && h0 + tid < a.H) s_head[tid] = head * a.sh;
   }
-  for (int h = kMaxTileSlots + tid; h < a.HG && h0 + h < a.H; h += threads_of(D))
+  for (int h = kMaxTileSlots + tid; h < a.HG && h0 + h < a.H; h += threads_of(D, I))
     s_head[h] = a.heads[h0 + h] * a.sh;
 }
 
 // One tile per workgroup.
 template <typename T, int D, int I>
-__global__ __launch_bounds__(threads_of(D)) void move_rows(RowsArgs a) {
+__global__ __launch_bounds__(threads_of(D, I)) void move_rows(RowsArgs a) {
   __shared__ int64_t s_slot[kMaxTileSlots];  // byte offset of a slot's row in a layer, -1: none
   __shared__ int64_t s_head[kMaxHeads];      // byte offset of a head slot in a row group
+  __shared__ int64_t s_src[I == kByPairs ? kMaxTileSlots : 1];  // kByPairs: staged row of a slot
 
   const TileId id = tile_id(a, xcd_tile(blockIdx.x, gridDim.x, a.xcd_chunk));
   const int64_t t0 = static_cast<int64_t>(id.tile) * a.TS;
@@ -354,9 +408,9 @@ __global__ __launch_bounds__(threads_of(D)) void move_rows(RowsArgs a) {
   // keep this uniform read scalar (the store might alias it), and a vector read of it made every
   // pass wait for all memory operations in flight (measured 8 % slower).
   const int64_t layer_base = a.layer_ptrs[id.layer];
-  tile_offsets<D, I>(a, id, t0, s_slot, s_head);
+  tile_offsets<D, I>(a, id, t0, s_slot, s_head, s_src);
   __syncthreads();
-  move_tile<T, D>(a, s_slot, s_head, layer_base, id.layer, id.group, t0);
+  move_tile<T, D, I>(a, s_slot, s_head, s_src, layer_base, id.layer, id.group, t0);
 }
 
 struct RowsCall {
@@ -374,16 +428,20 @@ struct RowsCall {
   const int64_t* strides;
   int64_t elem;
   int64_t* slots_out;
+  const int64_t* rows_of;
   hipStream_t stream;
 };
 
 template <int D, int I, typename T>
 int launch_typed(RowsArgs a, int64_t L, uint32_t W, hipStream_t stream, const char* name) {
-  const int64_t target = D == kGather ? EVS_GATHER_TILE_WORDS : EVS_SCATTER_TILE_WORDS;
-  const int hpt = D == kGather ? EVS_GATHER_HEADS_PER_TILE : EVS_SCATTER_HEADS_PER_TILE;
+  const int64_t target = I == kByPairs ? EVS_PAIRS_TILE_WORDS
+                         : D == kGather ? EVS_GATHER_TILE_WORDS : EVS_SCATTER_TILE_WORDS;
+  const int hpt = I == kByPairs ? EVS_PAIRS_HEADS_PER_TILE
+                  : D == kGather ? EVS_GATHER_HEADS_PER_TILE : EVS_SCATTER_HEADS_PER_TILE;
   a.HG = (hpt > 0 && hpt < a.H) ? hpt : a.H;
   a.group_fastest = D == kGather ? EVS_GATHER_GROUP_FASTEST : EVS_SCATTER_GROUP_FASTEST;
-  a.xcd_chunk = D == kGather ? EVS_GATHER_XCD_CHUNK : EVS_SCATTER_XCD_CHUNK;
+  a.xcd_chunk = I == kByPairs ? EVS_PAIRS_XCD_CHUNK
+                : D == kGather ? EVS_GATHER_XCD_CHUNK : EVS_SCATTER_XCD_CHUNK;
   const int64_t groups = (a.H + a.HG - 1) / a.HG;
   const int64_t per_slot = static_cast<int64_t>(a.HG) * 2 * W;
   int64_t ts = target / per_slot;
@@ -403,7 +461,7 @@ int launch_typed(RowsArgs a, int64_t L, uint32_t W, hipStream_t stream, const ch
   a.div_tiles = FastDiv(static_cast<uint32_t>(tiles));
   a.div_groups = FastDiv(static_cast<uint32_t>(groups));
   hipLaunchKernelGGL((move_rows<T, D, I>), dim3(static_cast<uint32_t>(grid)),
-                     dim3(threads_of(D)), 0, stream, a);
+                     dim3(threads_of(D, I)), 0, stream, a);
   EVS_LAUNCHED(name);
   return EVS_OK;
 }
@@ -418,12 +476,16 @@ int move(const RowsCall& c, const char* name) {
   EVS_REQUIRE(c.H <= kMaxHeads, "%s: at most %d head slots per call, got %lld", name, kMaxHeads,
               static_cast<long long>(c.H));
   const int64_t n = I == kByBlocks ? c.n_index * c.bs : c.n_index;
-  EVS_REQUIRE(n <= c.cap, "%s: more slots (%lld) than the staging capacity (%lld)", name,
+  // a pair names its staged row, so pairs may outnumber the rows (a row written to several slots)
+  EVS_REQUIRE(I == kByPairs || n <= c.cap,
+              "%s: more slots (%lld) than the staging capacity (%lld)", name,
               static_cast<long long>(n), static_cast<long long>(c.cap));
+  EVS_REQUIRE(c.cap >= 0, "%s: negative capacity", name);
   if (n == 0 || c.H == 0 || c.L == 0) return EVS_OK;
   EVS_REQUIRE(c.layer_ptrs != nullptr && c.heads != nullptr && c.rows != nullptr,
               "%s: null pointer", name);
   EVS_REQUIRE(I == kByBlocks ? c.blocks != nullptr : c.slots != nullptr, "%s: null index", name);
+  EVS_REQUIRE(I != kByPairs || c.rows_of != nullptr, "%s: null row list", name);
 
   const int64_t e = c.elem;
   RowsArgs a{};
@@ -433,6 +495,7 @@ int move(const RowsCall& c, const char* name) {
   a.heads = c.heads;
   a.rows = c.rows;
   a.slots_out = c.slots_out;
+  a.rows_of = c.rows_of;
   a.n = n;
   a.cap = c.cap;
   a.half_bytes = c.d * e;
@@ -479,7 +542,7 @@ extern "C" int evs_gather_rows(const int64_t* layer_ptrs, int64_t num_layers,
   evs::clear_error();
   evs::RowsCall c{layer_ptrs, num_layers, slots, nullptr, num_slots, heads, num_heads,
                   static_cast<char*>(out), capacity, head_dim, block_size, strides, elem_size,
-                  nullptr, evs::as_stream(stream)};
+                  nullptr, nullptr, evs::as_stream(stream)};
   return evs::move<evs::kGather, evs::kBySlots>(c, "evs_gather_rows");
 }
 
@@ -492,7 +555,7 @@ extern "C" int evs_gather_blocks(const int64_t* layer_ptrs, int64_t num_layers,
   evs::clear_error();
   evs::RowsCall c{layer_ptrs, num_layers, nullptr, block_ids, num_blocks, heads, num_heads,
                   static_cast<char*>(out), capacity, head_dim, block_size, strides, elem_size,
-                  slots_out, evs::as_stream(stream)};
+                  slots_out, nullptr, evs::as_stream(stream)};
   return evs::move<evs::kGather, evs::kByBlocks>(c, "evs_gather_blocks");
 }
 
@@ -504,6 +567,18 @@ extern "C" int evs_scatter_rows(const int64_t* layer_ptrs, int64_t num_layers,
   evs::clear_error();
   evs::RowsCall c{layer_ptrs, num_layers, slots, nullptr, num_slots, heads, num_heads,
                   const_cast<char*>(static_cast<const char*>(in)), capacity, head_dim,
-                  block_size, strides, elem_size, nullptr, evs::as_stream(stream)};
+                  block_size, strides, elem_size, nullptr, nullptr, evs::as_stream(stream)};
   return evs::move<evs::kScatter, evs::kBySlots>(c, "evs_scatter_rows");
+}
+
+extern "C" int evs_scatter_pairs(const int64_t* layer_ptrs, int64_t num_layers,
+                                 const int64_t* slots, const int64_t* rows_of, int64_t num_pairs,
+                                 const int64_t* heads, int64_t num_heads, const void* in,
+                                 int64_t capacity, int64_t head_dim, int64_t block_size,
+                                 const int64_t* strides, int64_t elem_size, void* stream) {
+  evs::clear_error();
+  evs::RowsCall c{layer_ptrs, num_layers, slots, nullptr, num_pairs, heads, num_heads,
+                  const_cast<char*>(static_cast<const char*>(in)), capacity, head_dim,
+                  block_size, strides, elem_size, nullptr, rows_of, evs::as_stream(stream)};
+  return evs::move<evs::kScatter, evs::kByPairs>(c, "evs_scatter_pairs");
 }

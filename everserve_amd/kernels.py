@@ -146,6 +146,8 @@ _SIGNATURES: tuple[tuple[str, object, tuple], ...] = (
         (_P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _P, _I64, _P, _P),
     ),
     ("evs_scatter_rows", _I32, (_P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _P, _I64, _P)),
+    ("evs_scatter_pairs", _I32,
+     (_P, _I64, _P, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _P, _I64, _P)),
     ("evs_local_reduce", _I32, (_P, _P, _P, _P, _I64, ctypes.c_uint64, _I64, _P, _P, _P)),
     ("evs_slot_all_reduce", _I32,
      (_P, _P, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I32, _I64, _P)),
@@ -341,6 +343,46 @@ class Kernels:
             self._check(
                 self._lib.evs_scatter_rows(
                     lp, layer_ptrs.numel(), sp, slots.numel(), hp, heads.numel(), int(in_ptr),
+                    int(capacity), int(d), int(block_size), st, int(elem_size),
+                    _stream_of(slots.device),
+                )
+            )
+
+    def scatter_pairs(
+        self,
+        layer_ptrs,
+        slots,
+        rows_of,
+        heads,
+        in_ptr: int,
+        capacity: int,
+        d: int,
+        block_size: int,
+        strides: Sequence[int],
+        elem_size: int,
+    ) -> None:
+        """Write staged row ``rows_of[i]`` of [L, H, cap, 2, d] into the caches at ``slots[i]``.
+
+        :meth:`scatter_rows` with the staged row of each slot named, so the caller chooses the
+        order of the writes: slots listed in increasing order write each cache front to back.
+        A negative slot, or a row outside ``[0, capacity)``, moves nothing.
+        """
+        import torch
+
+        if len(strides) != 5:
+            raise RuntimeError("scatter_pairs: a layout is five strides")
+        if rows_of.numel() != slots.numel():
+            raise RuntimeError(f"scatter_pairs: {slots.numel()} slots but {rows_of.numel()} rows")
+        lp = _device_ptr(layer_ptrs, "scatter_pairs: layer_ptrs", torch.long)
+        sp = _device_ptr(slots, "scatter_pairs: slots", torch.long)
+        rp = _device_ptr(rows_of, "scatter_pairs: rows_of", torch.long)
+        hp = _device_ptr(heads, "scatter_pairs: heads", torch.long)
+        _one_device("scatter_pairs", layer_ptrs, slots, rows_of, heads)
+        st = (ctypes.c_int64 * 5)(*[int(s) for s in strides])
+        with torch.cuda.device(slots.device):
+            self._check(
+                self._lib.evs_scatter_pairs(
+                    lp, layer_ptrs.numel(), sp, rp, slots.numel(), hp, heads.numel(), int(in_ptr),
                     int(capacity), int(d), int(block_size), st, int(elem_size),
                     _stream_of(slots.device),
                 )

@@ -29,6 +29,30 @@ HEAD_STRIDE = 1_000
 """A table id is layer * 1000 + head slot (core/everserve/state/mirror.py:59)."""
 
 
+def destination_order(slots, block_size: int | None = None) -> tuple[np.ndarray, np.ndarray]:
+    """A restore's (slot, staged row) pairs by increasing slot: ``(slots_sorted, rows_of)``.
+
+    ``slots[t]`` is the cache slot staged row t goes to; a negative slot is padding and is dropped.
+    Handed to ``scatter_pairs``, the pairs write each layer's cache front to back, which on MI355X
+    is faster than writing in staged order when the staged order is a permutation of the cache's
+    (a spare's fresh cache under a new block table). When the slots are whole blocks, block-size
+    runs ``b * block_size + [0, block_size)``, only the blocks are ordered.
+    """
+    s = np.asarray(slots, dtype=np.int64).reshape(-1)
+    if block_size and block_size > 1 and s.size and s.size % block_size == 0:
+        runs = s.reshape(-1, block_size)
+        first = runs[:, 0]
+        if ((first >= 0).all() and not (first % block_size).any()
+                and (runs == first[:, None] + np.arange(block_size, dtype=np.int64)).all()):
+            blocks = np.argsort(first, kind="stable")
+            rows_of = (blocks[:, None] * block_size
+                       + np.arange(block_size, dtype=np.int64)).reshape(-1)
+            return s[rows_of], rows_of
+    keep = np.flatnonzero(s >= 0)
+    rows_of = keep[np.argsort(s[keep], kind="stable")]
+    return s[rows_of], rows_of
+
+
 @dataclass
 class Table:
     """One store table of the lost rank: its rows and the slots written in it.

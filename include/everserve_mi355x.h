@@ -100,6 +100,21 @@ int evs_scatter_rows(const int64_t* layer_ptrs, int64_t num_layers, const int64_
                      int64_t capacity, int64_t head_dim, int64_t block_size,
                      const int64_t* strides, int64_t elem_size, void* stream);
 
+/* The scatter by (slot, staged row) pairs: for every listed i, layer and head index h, write staged
+ * row rows_of[i] of [num_layers, num_heads, capacity, 2, head_dim] into the cache at slot slots[i]
+ * and head slot heads[h]. evs_scatter_rows is the case rows_of[i] = i. A negative slot, or a row
+ * outside [0, capacity), moves nothing. The kernel writes in listed order, all heads of a slot
+ * together, so a caller that lists its slots in increasing order writes each layer's cache front
+ * to back; for a restore into a cache whose block table is a permutation of the staged order
+ * (the spare's fresh cache) that is the faster order. Slots must be distinct, as for
+ * evs_scatter_rows. No counterpart in the reference: it is the restore's scatter
+ * (core/everserve/state/mirror.py:926-937) with the order of its writes chosen by the caller. */
+int evs_scatter_pairs(const int64_t* layer_ptrs, int64_t num_layers, const int64_t* slots,
+                      const int64_t* rows_of, int64_t num_pairs, const int64_t* heads,
+                      int64_t num_heads, const void* in, int64_t capacity, int64_t head_dim,
+                      int64_t block_size, const int64_t* strides, int64_t elem_size,
+                      void* stream);
+
 /* The reduction stage of the failure-detecting all-reduce over member buffers already in this
  * GPU's HBM (the local stage of core/csrc/slot.cu:118-224):
  *

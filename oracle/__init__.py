@@ -16,6 +16,10 @@ gather_rows                core/csrc/gather.cu:29-47,                  brute for
                                                                        tests' literal shapes
 scatter_rows               core/everserve/state/kvcopy.py:118-128,     round trips, untouched rows,
                            core/everserve/state/mirror.py:926-937      torch index_put per layout
+scatter_pairs              scatter_rows with each slot's staged row    scatter_rows at rows_of = i
+                           named (no reference counterpart)            and on permuted rows; the
+                                                                       brute-force gather of what
+                                                                       it wrote; skipped pairs
 member_sum                 core/everserve/reference/arith/ops.py:63-73 torch's own .to(bfloat16)
                                                                        on fp32 sums, exact integer
                                                                        sums, rounding edge cases,
@@ -82,6 +86,8 @@ def lib() -> ctypes.CDLL:
         L.orc_gather_rows.restype = None
         L.orc_scatter_rows.argtypes = [P, I64, P, I64, P, I64, P, I64, I64, I64, P, I64]
         L.orc_scatter_rows.restype = None
+        L.orc_scatter_pairs.argtypes = [P, I64, P, P, I64, P, I64, P, I64, I64, I64, P, I64]
+        L.orc_scatter_pairs.restype = None
         L.orc_member_sum_bf16.argtypes = [P, I64, P, I64]
         L.orc_member_sum_bf16.restype = None
         L.orc_float_to_bf16.argtypes = [ctypes.c_float]
@@ -160,6 +166,27 @@ def scatter_rows(layers, slots, heads, rows, capacity: int, d: int, block_size: 
         _ptr_array([t.data_ptr() for t in layers]), len(layers), slots.ctypes.data, len(slots),
         heads.ctypes.data, len(heads), rows.ctypes.data, capacity, d, block_size, st.ctypes.data,
         elem,
+    )
+
+
+def scatter_pairs(layers, slots, rows_of, heads, rows, capacity: int, d: int, block_size: int,
+                  strides, elem: int) -> None:
+    """Write staged row ``rows_of[i]`` at ``slots[i]`` in the CPU ``layers``, in listed order.
+
+    A negative slot, or a row outside ``[0, capacity)``, writes nothing; :func:`scatter_rows` is
+    the case ``rows_of[i] = i``.
+    """
+    slots = np.ascontiguousarray(np.asarray(slots, dtype=np.int64))
+    rows_of = np.ascontiguousarray(np.asarray(rows_of, dtype=np.int64))
+    if rows_of.shape != slots.shape:
+        raise ValueError(f"{slots.size} slots but {rows_of.size} rows")
+    heads = np.ascontiguousarray(np.asarray(heads, dtype=np.int64))
+    st = np.ascontiguousarray(np.asarray(strides, dtype=np.int64))
+    rows = np.ascontiguousarray(rows)
+    lib().orc_scatter_pairs(
+        _ptr_array([t.data_ptr() for t in layers]), len(layers), slots.ctypes.data,
+        rows_of.ctypes.data, len(slots), heads.ctypes.data, len(heads), rows.ctypes.data,
+        capacity, d, block_size, st.ctypes.data, elem,
     )
 
 

@@ -65,6 +65,36 @@ void orc_scatter_rows(void* const* layers, int64_t L, const int64_t* slots, int6
   }
 }
 
+/*
+ * scatter by pairs: for i = 0 .. n-1, in listed order, staged row rows_of[i] is written at slot
+ * slots[i] exactly as orc_scatter_rows writes row t at slots[t]; a negative slot, or a row
+ * outside [0, capacity), writes nothing. orc_scatter_rows is the case rows_of[i] = i. The
+ * reference has no such call: it is its restore write (kvcopy.py:118-128) with the staged row of
+ * each slot named, so that a caller can choose the order of the writes.
+ */
+void orc_scatter_pairs(void* const* layers, int64_t L, const int64_t* slots,
+                       const int64_t* rows_of, int64_t n, const int64_t* heads, int64_t H,
+                       const void* rows, int64_t capacity, int64_t d, int64_t bs, const int64_t* S,
+                       int64_t elem) {
+  const unsigned char* in = (const unsigned char*)rows;
+  for (int64_t l = 0; l < L; l++) {
+    unsigned char* dst = (unsigned char*)layers[l];
+    for (int64_t h = 0; h < H; h++) {
+      for (int64_t i = 0; i < n; i++) {
+        int64_t s = slots[i], t = rows_of[i];
+        if (s < 0 || t < 0 || t >= capacity) continue;
+        for (int64_t k = 0; k < 2; k++) {
+          for (int64_t j = 0; j < d; j++) {
+            int64_t at = (s / bs) * S[0] + (s % bs) * S[1] + heads[h] * S[2] + k * S[3] + j * S[4];
+            int64_t from = ((((l * H + h) * capacity + t) * 2 + k) * d + j);
+            memcpy(dst + at * elem, in + from * elem, (size_t)elem);
+          }
+        }
+      }
+    }
+  }
+}
+
 static float bf16_to_float(uint16_t b) {
   uint32_t u = (uint32_t)b << 16;
   float f;

@@ -185,3 +185,88 @@ def test_the_reduce_of_no_members_is_zeros_and_of_no_elements_completes(ext):
     assert not out.any()
     empty = torch.empty(0, dtype=torch.bfloat16, device="cuda")
     reduce_call(ext, [x[:0] for x in xs], [0, 1], empty)
+
+
+def random_pairs(n: int, cap: int, seed: int):
+    """n pairs over distinct slots, with padding slots, rows outside [0, cap) and rows named
+    twice (one staged row written to two slots)."""
+    rng = np.random.default_rng(seed)
+    slots = rng.choice(NB * BS, size=n, replace=False).astype(np.int64)
+    rows_of = rng.integers(0, cap, size=n).astype(np.int64)
+    slots[rng.random(n) < 0.1] = -1
+    bad = rng.random(n) < 0.1
+    rows_of[bad] = np.where(rng.random(int(bad.sum())) < 0.5, -3, cap + 2)
+    return slots, rows_of
+
+
+@pytest.mark.parametrize("layout", LAYOUTS)
+@pytest.mark.parametrize("d", [8, 6])
+@pytest.mark.parametrize("n", [1, 2, 3, 9, 65, 300])
+def test_scatter_pairs_matches_the_oracle(ext, layout, d, n):
+    src = caches(layout, d, torch.bfloat16, n_layers=L, nb=NB, h=H, seed=300 + n)
+    cap = max(4, n // 2)  # fewer staged rows than pairs: some rows go to several slots
+    rows = oracle.gather_rows(src, ragged_slots(cap, n), [0, 1, 2], cap, d, BS,
+                              strides_of(src[0]), 2)
+    slots, rows_of = random_pairs(n, cap, n)
+    dst = caches(layout, d, torch.bfloat16, n_layers=L, nb=NB, h=H, seed=400 + n)
+    heads = [2, 0, 1]
+    want = [t.clone() for t in dst]
+    oracle.scatter_pairs(want, slots, rows_of, heads, rows, cap, d, BS, strides_of(want[0]), 2)
+    gpu = [t.cuda() for t in dst]
+    r = torch.from_numpy(rows.view(np.int16).copy()).cuda()
+    ext.scatter_pairs(ptrs(gpu), dev_long(slots), dev_long(rows_of), dev_long(heads), r.data_ptr(),
+                      cap, d, BS, list(strides_of(gpu[0])), 2)
+    torch.cuda.synchronize()
+    for g, w in zip(gpu, want):
+        assert np.array_equal(bits(g), bits(w))
+
+
+def test_scatter_pairs_in_destination_order_equals_the_scatter(ext):
+    """A permuted block table restored through destination_order + scatter_pairs writes the same
+    caches as scatter_rows in staged order."""
+    from everserve_amd.state.restore import destination_order
+
+    nb, h, d = 64, 4, 128
+    g = torch.Generator().manual_seed(21)
+    layers = [torch.zeros((2, nb, BS, h, d), dtype=torch.bfloat16).cuda() for _ in range(3)]
+    blocks = np.random.default_rng(21).permutation(nb)[:48]
+    slots = oracle.expand_blocks(blocks, BS)
+    n = len(slots)
+    rows = torch.randn((3, h, n, 2, d), generator=g).to(torch.bfloat16).cuda()
+    heads = dev_long(range(h))
+    st = list(strides_of(layers[0]))
+    ext.scatter_rows(ptrs(layers), dev_long(slots), heads, rows.data_ptr(), n, d, BS, st, 2)
+    torch.cuda.synchronize()
+    want = [t.clone() for t in layers]
+    for t in layers:
+        t.zero_()
+    sorted_slots, rows_of = destination_order(slots, block_size=BS)
+    assert (np.diff(sorted_slots) > 0).all()
+    ext.scatter_pairs(ptrs(layers), dev_long(sorted_slots), dev_long(rows_of), heads,
+                      rows.data_ptr(), n, d, BS, st, 2)
+    torch.cuda.synchronize()
+    for a, b in zip(layers, want):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+def test_scatter_pairs_fp8_and_empty(ext):
+    layers = caches("blocks_first", 8, torch.float8_e5m2, n_layers=L, nb=NB, h=H, seed=5)
+    cap = 40
+    rows = oracle.gather_rows(layers, ragged_slots(cap, 5), [0, 1, 2], cap, 8, BS,
+                              strides_of(layers[0]), 1)
+    slots, rows_of = random_pairs(33, cap, 5)
+    dst = [torch.zeros_like(t) for t in layers]
+    want = [t.clone() for t in dst]
+    oracle.scatter_pairs(want, slots, rows_of, [0, 1, 2], rows, cap, 8, BS, strides_of(want[0]), 1)
+    gpu = [t.cuda() for t in dst]
+    r = torch.from_numpy(rows.copy()).cuda()
+    ext.scatter_pairs(ptrs(gpu), dev_long(slots), dev_long(rows_of), dev_long([0, 1, 2]),
+                      r.data_ptr(), cap, 8, BS, list(strides_of(gpu[0])), 1)
+    ext.scatter_pairs(ptrs(gpu), dev_long(slots)[:0], dev_long(rows_of)[:0], dev_long([0, 1, 2]),
+                      r.data_ptr(), cap, 8, BS, list(strides_of(gpu[0])), 1)
+    torch.cuda.synchronize()
+    for g, w in zip(gpu, want):
+        assert np.array_equal(bits(g), bits(w))
+    with pytest.raises(RuntimeError, match="slots but"):
+        ext.scatter_pairs(ptrs(gpu), dev_long(slots), dev_long(rows_of[:-1]), dev_long([0]),
+                          r.data_ptr(), cap, 8, BS, list(strides_of(gpu[0])), 1)

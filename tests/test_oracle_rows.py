@@ -13,8 +13,8 @@ import torch
 
 import oracle
 from oracle import cpu_path
-from tests.cases import (CAPACITY, DTYPES, HEADS, LAYOUTS, SLOTS, bits, brute_gather, caches,
-                         strides_of)
+from tests.cases import (BS, CAPACITY, DTYPES, H, HEADS, LAYOUTS, NB, SLOTS, bits, brute_gather,
+                         caches, strides_of)
 
 
 def oracle_gather(layers, slots, heads, capacity=CAPACITY, strides=None):
@@ -125,3 +125,54 @@ def test_layout_strides_follow_the_tensor():
     assert strides_of(c) == (192, 48, 16, 8, 1)
     with pytest.raises(ValueError):
         oracle.recognise((3, 3, 3))
+
+
+PAIR_SLOTS = [17, 5, -1, 27, 0, 9]
+PAIR_ROWS = [3, 0, 1, 4, 9, 3]  # row 9 lies outside CAPACITY: that pair writes nothing
+
+
+@pytest.mark.parametrize("layout", LAYOUTS)
+@pytest.mark.parametrize("d", [8, 6])
+def test_scatter_pairs_at_the_identity_is_the_scatter(layout, d):
+    src = caches(layout, d, torch.bfloat16, seed=11)
+    staged = oracle_gather(src, SLOTS, HEADS)
+    _, _, bs, _ = oracle.recognise(src[0].shape)
+    a = [torch.zeros_like(t) for t in src]
+    b = [torch.zeros_like(t) for t in src]
+    oracle.scatter_rows(a, SLOTS, HEADS, staged, CAPACITY, d, bs, strides_of(a[0]), 2)
+    oracle.scatter_pairs(b, SLOTS, range(len(SLOTS)), HEADS, staged, CAPACITY, d, bs,
+                         strides_of(b[0]), 2)
+    for x, y in zip(a, b):
+        assert np.array_equal(bits(x), bits(y))
+
+
+@pytest.mark.parametrize("layout", LAYOUTS)
+@pytest.mark.parametrize("d", [8, 6])
+def test_scatter_pairs_writes_the_named_rows_and_nothing_else(layout, d):
+    src = caches(layout, d, torch.bfloat16, seed=12)
+    staged = oracle_gather(src, list(range(CAPACITY)), HEADS)  # 8 distinct staged rows
+    _, _, bs, _ = oracle.recognise(src[0].shape)
+    dst = [torch.zeros_like(t) for t in src]
+    oracle.scatter_pairs(dst, PAIR_SLOTS, PAIR_ROWS, HEADS, staged, CAPACITY, d, bs,
+                         strides_of(dst[0]), 2)
+    # the brute force (by tensor dimension, not by strides) reads back exactly the named rows
+    kept = [(s, r) for s, r in zip(PAIR_SLOTS, PAIR_ROWS) if s >= 0 and 0 <= r < CAPACITY]
+    back = brute_gather(dst, [s for s, _ in kept], HEADS, len(kept))
+    assert np.array_equal(back, staged[:, :, [r for _, r in kept]])
+    # the same as the plain scatter of the rows in pair order
+    again = [torch.zeros_like(t) for t in src]
+    oracle.scatter_rows(again, [s for s, _ in kept], HEADS,
+                        np.ascontiguousarray(staged[:, :, [r for _, r in kept]]), len(kept), d, bs,
+                        strides_of(again[0]), 2)
+    for x, y in zip(dst, again):
+        assert np.array_equal(bits(x), bits(y))
+    # and nothing else: every other element is still zero
+    touched = sum(int((bits(t) != 0).sum()) for t in dst)
+    assert touched == int((back != 0).sum())
+
+
+def test_scatter_pairs_refuses_mismatched_lists():
+    dst = [torch.zeros(2, NB, BS, H, 8, dtype=torch.bfloat16)]
+    with pytest.raises(ValueError):
+        oracle.scatter_pairs(dst, [1, 2], [0], [0], np.zeros((1, 1, 8, 2, 8), np.uint16), 8, 8,
+                             BS, strides_of(dst[0]), 2)

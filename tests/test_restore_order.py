@@ -1,0 +1,50 @@
+"""The host side of the ordered restore: ``destination_order`` on the CPU.
+
+The pairs it returns must name every non-padding staged row exactly once, in increasing slot
+order; the whole-block fast path must return what the generic sort returns.
+"""
+
+import numpy as np
+import pytest
+
+from everserve_amd.state.restore import destination_order
+
+
+def check(slots, got_slots, rows_of):
+    slots = np.asarray(slots, dtype=np.int64)
+    keep = np.flatnonzero(slots >= 0)
+    assert sorted(rows_of.tolist()) == keep.tolist()
+    assert np.array_equal(got_slots, slots[rows_of])
+    assert (np.diff(got_slots) >= 0).all()
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_any_slot_list_comes_back_sorted_without_padding(seed):
+    rng = np.random.default_rng(seed)
+    slots = rng.choice(10_000, size=777, replace=False).astype(np.int64)
+    slots[rng.random(777) < 0.1] = -1
+    check(slots, *destination_order(slots))
+    check(slots, *destination_order(slots, block_size=16))
+
+
+@pytest.mark.parametrize("bs", [1, 4, 16])
+def test_whole_blocks_order_the_blocks_and_match_the_generic_sort(bs):
+    blocks = np.random.default_rng(4).permutation(512)
+    slots = (blocks[:, None] * bs + np.arange(bs)).reshape(-1)
+    fast = destination_order(slots, block_size=bs)
+    generic = destination_order(slots)
+    assert np.array_equal(fast[0], generic[0]) and np.array_equal(fast[1], generic[1])
+    assert np.array_equal(fast[0], np.arange(512 * bs))
+
+
+def test_runs_that_are_not_whole_blocks_take_the_generic_path():
+    slots = np.array([5, 6, 7, 8, 0, 1, 2, 3], dtype=np.int64)  # the first run starts mid-block
+    got, rows_of = destination_order(slots, block_size=4)
+    check(slots, got, rows_of)
+    assert got.tolist() == [0, 1, 2, 3, 5, 6, 7, 8]
+
+
+def test_empty_and_all_padding():
+    for slots in ([], [-1, -1, -1, -1]):
+        got, rows_of = destination_order(slots, block_size=4)
+        assert got.size == 0 and rows_of.size == 0
