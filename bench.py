@@ -455,9 +455,29 @@ def bench_c4(ext, steps, warmup):
     ext.gather_rows(ptrs[:4], s, heads, back.data_ptr(), n, D, BS, strides, 2)
     torch.cuda.synchronize()
     ok = bool(torch.equal(back.view(torch.int16), rows[:4].view(torch.int16)))
+
+    # the same restore with its writes in cache order: the (slot, staged row) pairs sorted by slot
+    # on the host from the block table, then scatter_pairs
+    from everserve_amd.state.restore import destination_order
+
+    t0 = time.perf_counter()
+    o_slots, o_rows = destination_order(slots, block_size=BS)
+    order_ms = (time.perf_counter() - t0) * 1e3
+    os_dev, or_dev = torch.from_numpy(o_slots).to(dev), torch.from_numpy(o_rows).to(dev)
+
+    def ordered():
+        ext.scatter_pairs(ptrs, os_dev, or_dev, heads, rows.data_ptr(), n, D, BS, strides, 2)
+
+    for t in caches[:4]:
+        t.zero_()
+    per_o, _ = time_launches(ordered, steps, warmup, stream)
+    ext.gather_rows(ptrs[:4], s, heads, back.data_ptr(), n, D, BS, strides, 2)
+    torch.cuda.synchronize()
+    ok_o = bool(torch.equal(back.view(torch.int16), rows[:4].view(torch.int16)))
     del rows, caches, back
     torch.cuda.empty_cache()
     ms = sum(per) / len(per)
+    ms_o = sum(per_o) / len(per_o)
     return {
         "config": "C4 restore: [32,8,262144,2,128] bf16 rows into a fresh 16384-block cache, "
                   "random-permutation block table (64 seqs x 4096 tokens)",
@@ -465,6 +485,15 @@ def bench_c4(ext, steps, warmup):
         "scatter_gbs": round(2 * payload / ms / 1e6, 1),
         "scatter_frac_of_8tbs": round(2 * payload / ms / 1e6 / PEAK_HBM_GBS, 4),
         "round_trip_equal_first_4_layers": ok,
+        "ordered": {
+            "how": "scatter_pairs with the pairs in slot order (destination_order on the host: "
+                   "the block table's 16,384 blocks sorted)",
+            "scatter_ms": round(ms_o, 3),
+            "scatter_gbs": round(2 * payload / ms_o / 1e6, 1),
+            "scatter_frac_of_8tbs": round(2 * payload / ms_o / 1e6 / PEAK_HBM_GBS, 4),
+            "order_host_ms": round(order_ms, 2),
+            "round_trip_equal_first_4_layers": ok_o,
+        },
     }
 
 
