@@ -126,6 +126,24 @@ def test_256_head_slots_in_one_call_and_257_refused(ext):
     with pytest.raises(KernelError, match="head slots"):
         ext.gather_rows(ptrs(gpu), dev_long(slots), dev_long(order + [0]), out.data_ptr(), 4,
                         d, BS, list(strides_of(gpu[0])), 2)
+    # both scatters write the 256 head slots back: a pair tile spans them all in 16 passes, and
+    # its head offsets past the first wave's 64 come from the fill loop
+    r = torch.from_numpy(want.view(np.int16).copy()).cuda()
+    for how in ("rows", "pairs"):
+        dst = [torch.zeros_like(t) for t in gpu]
+        ref = [torch.zeros_like(t) for t in layers]
+        live = [s for s in slots if s >= 0]
+        if how == "rows":
+            ext.scatter_rows(ptrs(dst), dev_long(slots), dev_long(order), r.data_ptr(), 4, d, BS,
+                             list(strides_of(dst[0])), 2)
+            oracle.scatter_rows(ref, slots, order, want, 4, d, BS, strides_of(ref[0]), 2)
+        else:
+            ext.scatter_pairs(ptrs(dst), dev_long(slots[::-1]), dev_long([3, 2, 1, 0]),
+                              dev_long(order), r.data_ptr(), 4, d, BS, list(strides_of(dst[0])), 2)
+            oracle.scatter_pairs(ref, slots[::-1], [3, 2, 1, 0], order, want, 4, d, BS,
+                                 strides_of(ref[0]), 2)
+        torch.cuda.synchronize()
+        assert live and all(np.array_equal(bits(a), bits(b)) for a, b in zip(dst, ref))
 
 
 def test_fp8_e5m2_moves_as_raw_bytes(ext):
