@@ -12,6 +12,7 @@ import pytest
 import torch
 
 import oracle
+from everserve_amd.state.restore import destination_order
 from tests.cases import (CAPACITY, DTYPES, HEADS, LAYOUTS, SLOTS, bits, caches, strides_of)
 
 pytestmark = pytest.mark.gpu
@@ -240,7 +241,8 @@ def test_copy_rows_moves_only_the_filled_rows(ext):
 
 def test_c4_restore_round_trip_full_size(ext):
     """C4: 64 seqs x 4096 tokens of Llama-3-8B rows (32 GiB) scattered into a fresh
-    16384-block cache through a seeded random-permutation block table, gathered back: equal."""
+    16384-block cache through a seeded random-permutation block table, gathered back: equal,
+    through both scatters."""
     L, NB, BS, H, D = 32, 16384, 16, 8, 128
     n = NB * BS
     rows = torch.empty((L, H, n, 2, D), dtype=torch.bfloat16, device="cuda")
@@ -250,10 +252,22 @@ def test_c4_restore_round_trip_full_size(ext):
     s = torch.from_numpy(slots).cuda()
     heads = torch.arange(H, dtype=torch.long, device="cuda")
     strides = list(strides_of(cache[0]))
-    ext.scatter_rows(ptrs(cache), s, heads, rows.data_ptr(), n, D, BS, strides, 2)
     back = torch.empty((8, H, n, 2, D), dtype=torch.bfloat16, device="cuda")
-    for first in range(0, L, 8):
-        ext.gather_rows(ptrs(cache[first:first + 8]), s, heads, back.data_ptr(), n, D, BS,
-                        strides, 2)
-        torch.cuda.synchronize()
-        assert torch.equal(back.view(torch.int16), rows[first:first + 8].view(torch.int16)), first
+    # in staged order (scatter_rows), then the same restore in cache order (scatter_pairs with
+    # the pairs destination_order sorts from the block table), each into zeroed caches
+    sorted_slots, rows_of = destination_order(slots, block_size=BS)
+    for how in ("staged order", "cache order"):
+        for t in cache:
+            t.zero_()
+        if how == "staged order":
+            ext.scatter_rows(ptrs(cache), s, heads, rows.data_ptr(), n, D, BS, strides, 2)
+        else:
+            ext.scatter_pairs(ptrs(cache), torch.from_numpy(sorted_slots).cuda(),
+                              torch.from_numpy(rows_of).cuda(), heads, rows.data_ptr(), n, D, BS,
+                              strides, 2)
+        for first in range(0, L, 8):
+            ext.gather_rows(ptrs(cache[first:first + 8]), s, heads, back.data_ptr(), n, D, BS,
+                            strides, 2)
+            torch.cuda.synchronize()
+            assert torch.equal(back.view(torch.int16),
+                               rows[first:first + 8].view(torch.int16)), (how, first)
