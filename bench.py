@@ -927,6 +927,17 @@ def main(argv=None):
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for "
               f"--gpus {a.gpus}); run it with --gpus 1", file=sys.stderr)
         return 2
+    legs = (("c1_gather", bench_c1), ("c2_layouts", bench_c2_layouts),
+            ("c3_fp8_gather_d2h", bench_c3),
+            ("c4_restore", bench_c4),
+            ("restore_host_path", bench_restore_host), ("store_commit", bench_store_commit),
+            ("c5_reduce", bench_c5),
+            ("slot_all_reduce", bench_slot), ("decode_overhead", bench_decode_overhead))
+    wanted = {x for x in a.legs.split(",") if x}
+    unknown = wanted - {name for name, _ in legs}
+    if unknown:
+        print(f"unknown legs: {sorted(unknown)}", file=sys.stderr)
+        return 2
 
     import torch
 
@@ -982,17 +993,6 @@ def main(argv=None):
         result["extra"]["c2_gather_blocks"] = {
             "ms": round(bms, 4), "gbs": round(c2["algo_bytes"] / bms / 1e6, 1),
             "rows_equal_gather_rows": c2["blocks_equal"]}
-    legs = (("c1_gather", bench_c1), ("c2_layouts", bench_c2_layouts),
-            ("c3_fp8_gather_d2h", bench_c3),
-            ("c4_restore", bench_c4),
-            ("restore_host_path", bench_restore_host), ("store_commit", bench_store_commit),
-            ("c5_reduce", bench_c5),
-            ("slot_all_reduce", bench_slot), ("decode_overhead", bench_decode_overhead))
-    wanted = {x for x in a.legs.split(",") if x}
-    unknown = wanted - {name for name, _ in legs}
-    if unknown:
-        print(f"unknown legs: {sorted(unknown)}", file=sys.stderr)
-        return 2
     if not a.quick:
         for name, fn in legs:
             if wanted and name not in wanted:
