@@ -835,6 +835,49 @@ def bench_decode_overhead(ext, steps, warmup):
 
 
 # ------------------------------------------------------------------------------ counter runs
+def pcie_workload(ext, copies=5):
+    """What a rocprofv3 memory-copy trace measures: the host copies of the path, each beside a
+    plain copy of the same size (torch's copy of a contiguous tensor, one hipMemcpyAsync).
+
+    D2H: C3's staged rows, 80 groups of 8 MiB (640 MiB), by ``evs_copy_rows_async`` as the step
+    path issues it. H2D: the restore's 64 MiB chunks by ``evs_copy_rows_async``, 16 of them
+    (1 GiB), and one plain 1 GiB copy. Prints one line of HIP-event rates.
+    """
+    import torch
+
+    dev = torch.device("cuda", 0)
+    stream = torch.cuda.current_stream(dev)
+    group, groups = 32768 * 256, 80
+    d = torch.empty(group * groups, dtype=torch.uint8, device=dev)
+    h = torch.empty(group * groups, dtype=torch.uint8, pin_memory=True)
+    chunk, chunks = 64 << 20, 16
+    d2 = torch.empty(chunk * chunks, dtype=torch.uint8, device=dev)
+    h2 = torch.empty(chunk * chunks, dtype=torch.uint8, pin_memory=True)
+
+    def rows_d2h():
+        ext.copy_rows_async(h.data_ptr(), d.data_ptr(), groups, group, group, dev)
+
+    def plain_d2h():
+        h.copy_(d, non_blocking=True)
+
+    def chunks_h2d():
+        for c in range(chunks):
+            ext.copy_rows_async(d2.data_ptr() + c * chunk, h2.data_ptr() + c * chunk, 1, chunk,
+                                chunk, dev)
+
+    def plain_h2d():
+        d2.copy_(h2, non_blocking=True)
+
+    out = {}
+    for name, fn, nbytes in (("d2h_rows", rows_d2h, d.numel()), ("d2h_plain", plain_d2h, d.numel()),
+                             ("h2d_chunks", chunks_h2d, d2.numel()),
+                             ("h2d_plain", plain_h2d, d2.numel())):
+        per, _ = time_launches(fn, copies, 1, stream)
+        out[name + "_gbs"] = round(nbytes / (sum(per) / len(per)) / 1e6, 2)
+    torch.cuda.synchronize()
+    print(json.dumps({"pcie_workload": out}), flush=True)
+
+
 def pmc_workload(ext, which="gather", launches=5):
     """What the rocprofv3 counter runs measure: ``launches`` calls of one kernel, then
     ``launches`` copies of a 1 GiB bf16 tensor by an elementwise kernel (torch.neg) whose
@@ -918,6 +961,9 @@ def main(argv=None):
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--legs", default="",
                     help="comma-separated extra legs to run (default: all; --quick: none)")
+    ap.add_argument("--pcie", action="store_true",
+                    help="only the host copies of the path beside plain copies, for a "
+                         "rocprofv3 memory-copy trace")
     ap.add_argument("--pmc", nargs="?", const="gather", default=None,
                     choices=("gather", "scatter", "reduce"),
                     help="only a counter run's workload: 5 calls of the named kernel (default "
@@ -947,6 +993,9 @@ def main(argv=None):
     torch.cuda.set_device(0)
     if a.pmc:
         pmc_workload(ext, a.pmc)
+        return 0
+    if a.pcie:
+        pcie_workload(ext)
         return 0
     log(f"device {torch.cuda.get_device_name(0)}; library {ext.__file__}")
 
