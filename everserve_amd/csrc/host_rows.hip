@@ -38,23 +38,35 @@ void copy_rows(const char* src, int64_t row_bytes, const int64_t* starts, const 
 }  // namespace
 }  // namespace evs
 
-extern "C" int evs_host_gather_ranges(const void* src, int64_t row_bytes, const int64_t* starts,
-                                      const int64_t* counts, int64_t nranges, void* dst,
+extern "C" int evs_host_gather_ranges(const void* src, int64_t src_rows, int64_t row_bytes,
+                                      const int64_t* starts, const int64_t* counts,
+                                      int64_t nranges, void* dst, int64_t dst_rows,
                                       int64_t max_threads, int64_t* rows_out) {
   evs::clear_error();
-  EVS_REQUIRE(row_bytes > 0 && nranges >= 0 && max_threads >= 1,
-              "evs_host_gather_ranges: row_bytes > 0, nranges >= 0, max_threads >= 1");
+  if (rows_out != nullptr) *rows_out = 0;
+  EVS_REQUIRE(row_bytes > 0 && nranges >= 0 && max_threads >= 1 && src_rows >= 0 &&
+                  dst_rows >= 0,
+              "evs_host_gather_ranges: row_bytes > 0, nranges >= 0, max_threads >= 1 and "
+              "src_rows, dst_rows >= 0");
   EVS_REQUIRE(nranges == 0 || (src != nullptr && dst != nullptr && starts != nullptr &&
                                counts != nullptr),
               "evs_host_gather_ranges: null pointer");
+  // every range is checked before anything is copied
   std::vector<int64_t> first_row(static_cast<size_t>(nranges) + 1, 0);
   for (int64_t k = 0; k < nranges; k++) {
     EVS_REQUIRE(starts[k] >= 0 && counts[k] >= 0, "evs_host_gather_ranges: negative range %lld",
                 static_cast<long long>(k));
+    EVS_REQUIRE(starts[k] <= src_rows && counts[k] <= src_rows - starts[k],
+                "evs_host_gather_ranges: range %lld (%lld + %lld) lies outside the table's %lld rows",
+                static_cast<long long>(k), static_cast<long long>(starts[k]),
+                static_cast<long long>(counts[k]), static_cast<long long>(src_rows));
+    EVS_REQUIRE(counts[k] <= dst_rows - first_row[k],
+                "evs_host_gather_ranges: the ranges hold more rows than dst's %lld",
+                static_cast<long long>(dst_rows));
     first_row[k + 1] = first_row[k] + counts[k];
   }
   const int64_t rows = first_row[nranges];
-  if (rows_out != nullptr) *rows_out = rows;
+  if (rows_out != nullptr) *rows_out = rows;  // the copy below cannot fail
   if (rows == 0) return EVS_OK;
   const int64_t bytes = rows * row_bytes;
   int64_t threads = bytes / evs::kMinBytesPerThread;

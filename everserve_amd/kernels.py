@@ -160,7 +160,7 @@ _SIGNATURES: tuple[tuple[str, object, tuple], ...] = (
     ("evs_device_free", _I32, (_P,)),
     ("evs_memset_async", _I32, (_P, _I64, _P)),
     ("evs_copy_rows_async", _I32, (_P, _P, _I64, _I64, _I64, _P)),
-    ("evs_host_gather_ranges", _I32, (_P, _I64, _P, _P, _I64, _P, _I64, _P)),
+    ("evs_host_gather_ranges", _I32, (_P, _I64, _I64, _P, _P, _I64, _P, _I64, _I64, _P)),
     ("evs_store_commit", _I32,
      (_P, _I64, _P, _I64, _P, _P, _P, _I64, _I64, _P, _I64, ctypes.c_uint64, _I64, _P)),
     ("evs_crc32c", _I32, (_P, _I64, _P)),
@@ -400,11 +400,13 @@ class Kernels:
                                           int(pitch), _stream_of(dev))
         )
 
-    def host_gather_ranges(self, src_ptr: int, row_bytes: int, starts, counts, dst_ptr: int,
-                           max_threads: int = 16) -> int:
-        """Copy the rows of slot ranges of a host table into ``dst_ptr`` on host threads.
+    def host_gather_ranges(self, src_ptr: int, src_rows: int, row_bytes: int, starts, counts,
+                           dst_ptr: int, dst_rows: int, max_threads: int = 16) -> int:
+        """Copy the rows of slot ranges of a host table (``src_rows`` rows) into ``dst_ptr``
+        (room for ``dst_rows``) on host threads; returns the rows copied.
 
-        ``starts`` and ``counts`` are int64 numpy arrays; returns the rows copied.
+        ``starts`` and ``counts`` are int64 numpy arrays. A range outside the table, or more rows
+        than ``dst`` holds, is refused before anything is copied.
         """
         import numpy as np
 
@@ -414,9 +416,10 @@ class Kernels:
             raise RuntimeError("host_gather_ranges: starts and counts differ in length")
         rows = ctypes.c_int64()
         self._check(
-            self._lib.evs_host_gather_ranges(int(src_ptr), int(row_bytes), st.ctypes.data,
-                                             ct.ctypes.data, st.size, int(dst_ptr),
-                                             int(max_threads), ctypes.byref(rows))
+            self._lib.evs_host_gather_ranges(int(src_ptr), int(src_rows), int(row_bytes),
+                                             st.ctypes.data, ct.ctypes.data, st.size,
+                                             int(dst_ptr), int(dst_rows), int(max_threads),
+                                             ctypes.byref(rows))
         )
         return rows.value
 

@@ -152,7 +152,8 @@ class Restorer:
                 done = self._done[buf]
                 if done is not None:
                     done.synchronize()  # the copy out of this pinned buffer has finished
-                got = self._ext.host_gather_ranges(src, rb, st, ct, self._host[buf].data_ptr(),
+                got = self._ext.host_gather_ranges(src, table.rows.nbytes // rb, rb, st, ct,
+                                                   self._host[buf].data_ptr(), n_chunk,
                                                    self._threads)
                 assert got == c1 - c0
                 slots = self._host_slots[buf].numpy()

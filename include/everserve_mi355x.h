@@ -194,14 +194,15 @@ int evs_copy_rows_async(void* dst, const void* src, int64_t groups, int64_t byte
                         void* stream);
 
 /* The restore's host gather: copy the rows of `nranges` slot ranges (starts[k], counts[k]) of a
- * store table at `src` ([num_slots, row_bytes], a shared-memory mapping) into `dst`, one range
- * after another, on up to max_threads host threads; *rows_out (if not NULL) receives the row
- * count. Host memory only, no device call. Replaces the per-table torch.index_select of the
- * restore (core/everserve/state/mirror.py:926-932); the ranges are the table's written
- * SlotRanges (proto/everserve/proto/mirror.proto:102-117). */
-int evs_host_gather_ranges(const void* src, int64_t row_bytes, const int64_t* starts,
-                           const int64_t* counts, int64_t nranges, void* dst, int64_t max_threads,
-                           int64_t* rows_out);
+ * store table at `src` ([src_rows, row_bytes], a shared-memory mapping) into `dst` (room for
+ * dst_rows rows), one range after another, on up to max_threads host threads; *rows_out (if not
+ * NULL) receives the row count. Every range must lie within the table and all of them must fit
+ * in dst, or nothing is copied. Host memory only, no device call. Replaces the per-table
+ * torch.index_select of the restore (core/everserve/state/mirror.py:926-932); the ranges are the
+ * table's written SlotRanges (proto/everserve/proto/mirror.proto:102-117). */
+int evs_host_gather_ranges(const void* src, int64_t src_rows, int64_t row_bytes,
+                           const int64_t* starts, const int64_t* counts, int64_t nranges,
+                           void* dst, int64_t dst_rows, int64_t max_threads, int64_t* rows_out);
 
 /* The node store's commit copy (store/src/storage.rs:864-957; copy loop :916-943): the rows of
  * one staged step into `ntables` store tables, on the host.

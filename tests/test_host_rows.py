@@ -36,16 +36,31 @@ def test_the_rows_of_the_ranges_in_order(ext, num_slots, row_bytes, ranges):
     counts = np.array([c for _, c in ranges], dtype=np.int64)
     want = concat(table, row_bytes, starts, counts)
     dst = np.full(max(1, want.size), 0xEE, dtype=np.uint8)
-    rows = ext.host_gather_ranges(table.ctypes.data, row_bytes, starts, counts, dst.ctypes.data, 8)
+    rows = ext.host_gather_ranges(table.ctypes.data, num_slots, row_bytes, starts, counts,
+                                  dst.ctypes.data, dst.size // row_bytes, 8)
     assert rows == counts.sum()
     assert np.array_equal(dst[:want.size], want)
 
 
 def test_bad_ranges_are_refused(ext):
-    table = np.zeros(64, np.uint8)
-    dst = np.zeros(64, np.uint8)
+    table = np.zeros(64, np.uint8)  # 4 rows of 16 bytes
+    dst = np.full(64, 7, np.uint8)  # room for 4 rows
     with pytest.raises(kernels.KernelError, match="negative range"):
-        ext.host_gather_ranges(table.ctypes.data, 16, np.array([-1]), np.array([1]),
-                               dst.ctypes.data)
+        ext.host_gather_ranges(table.ctypes.data, 4, 16, np.array([-1]), np.array([1]),
+                               dst.ctypes.data, 4)
     with pytest.raises(kernels.KernelError, match="row_bytes"):
-        ext.host_gather_ranges(table.ctypes.data, 0, np.array([0]), np.array([1]), dst.ctypes.data)
+        ext.host_gather_ranges(table.ctypes.data, 4, 0, np.array([0]), np.array([1]),
+                               dst.ctypes.data, 4)
+    # past the table's end, by the start or by the count, and the largest count that overflows
+    for start, count in ((4, 1), (3, 2), (1, 2**62)):
+        with pytest.raises(kernels.KernelError, match="outside the table"):
+            ext.host_gather_ranges(table.ctypes.data, 4, 16, np.array([0, start]),
+                                   np.array([1, count]), dst.ctypes.data, 4)
+    # more rows than dst holds: refused before the first range is copied
+    with pytest.raises(kernels.KernelError, match="more rows than dst"):
+        ext.host_gather_ranges(table.ctypes.data, 4, 16, np.array([0, 1]), np.array([3, 2]),
+                               dst.ctypes.data, 4)
+    assert (dst == 7).all()
+    # the whole table into exactly enough room is fine
+    assert ext.host_gather_ranges(table.ctypes.data, 4, 16, np.array([0]), np.array([4]),
+                                  dst.ctypes.data, 4) == 4
