@@ -66,12 +66,17 @@ static_assert(kGroupStride * (1 + kGroups) <= EVS_REDUCE_STATE_WORDS, "state rec
 // flag values returned, it sees what the producer wrote before releasing its flag. 1: one
 // acquire fence per workgroup (an L2 invalidate); 2: one per wave; 0: none, right only when every
 // payload was written before the launch.
+// The order of a thread's payload loads: 0 member by member, 1 vector by vector.
+#ifndef EVS_REDUCE_LOAD_ORDER
+#define EVS_REDUCE_LOAD_ORDER 1
+#endif
 #ifndef EVS_REDUCE_FENCE
 #define EVS_REDUCE_FENCE 3
 #endif
 // buffer-load cache policy: sc1 (coherent at agent scope), plus nt when the payload streams
 constexpr int kPayloadScope = 16 | ((EVS_REDUCE_NT & 1) ? 2 : 0);
 constexpr int kRsrcWord3 = 0x00020000;  // raw buffer resource, dword 3 (gfx9 untyped access)
+constexpr int kOutputPolicy = (EVS_REDUCE_NT & 2) ? 2 : 0;  // buffer-store cache policy: nt
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
@@ -108,6 +113,18 @@ __device__ __forceinline__ uint32_t f32_to_bf16(float f) {
   const uint32_t u = __float_as_uint(f);
   if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
   return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+// A buffer resource over `records` bytes from p (uniform across the wave): a raw, untyped view
+// whose loads past the end return zeros and whose stores past the end are dropped. The address
+// halves go through readfirstlane, which returns a signed int: each is kept as uint32_t before
+// the halves are joined, so a low half with bit 31 set does not spill ones into the high half.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const void* p, int records) {
+  const uint64_t a = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a >> 32));
+  return __builtin_amdgcn_make_buffer_rsrc(
+      reinterpret_cast<void*>((static_cast<uint64_t>(hi) << 32) | lo), 0, records, kRsrcWord3);
 }
 
 // Count one arrival with `outcome` in the counting word w: OR the outcome into the high bits, then
@@ -250,22 +267,51 @@ __global__ __launch_bounds__(kThreads) void local_reduce(ReduceArgs a) {
       // a buffer resource per member over this pass's vectors: a load past the end returns 0
       const int64_t left = (nvec - vb) * 16;
       const int records = static_cast<int>(left < (int64_t{1} << 30) ? left : (int64_t{1} << 30));
+      // an absent member (missing, or past the count) gets an empty resource: its loads return
+      // zeros without touching memory, so no branch separates the loads from their uses
+      __amdgpu_buffer_rsrc_t r[kMaxRows];
 #pragma unroll
-      for (int q = 0; q < kMaxRows; q++) {
-        const uint64_t base = reinterpret_cast<uint64_t>(src[q] + vb * 8);
-        const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(base));
-        const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(base >> 32));
-        __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
-            reinterpret_cast<void*>((static_cast<uint64_t>(hi) << 32) | lo), 0, records,
-            kRsrcWord3);
+      for (int q = 0; q < kMaxRows; q++)
+        r[q] = src[q] != nullptr ? uniform_rsrc(src[q] + vb * 8, records) : uniform_rsrc(a.out, 0);
+      // vector-major (1): vector i's loads from every member come before vector i + 1's, so its
+      // sum and store can go out while the later vectors' loads are still in flight
 #pragma unroll
-        for (int i = 0; i < kVpt; i++) {
-          x[i][q] = u32x4{0u, 0u, 0u, 0u};
-          if (src[q] != nullptr)
-            x[i][q] = __builtin_amdgcn_raw_buffer_load_b128(r, (i * kThreads + tid) * 16, 0,
-                                                            kPayloadScope);
-        }
+      for (int j = 0; j < kVpt * kMaxRows; j++) {
+        const int i = EVS_REDUCE_LOAD_ORDER ? j / kMaxRows : j % kVpt;
+        const int q = EVS_REDUCE_LOAD_ORDER ? j % kMaxRows : j / kVpt;
+        x[i][q] = __builtin_amdgcn_raw_buffer_load_b128(r[q], (i * kThreads + tid) * 16, 0,
+                                                        kPayloadScope);
+        // keep each vector's loads together, in this order (the scheduler would group them by
+        // member otherwise)
+        if (EVS_REDUCE_LOAD_ORDER && q == kMaxRows - 1) __builtin_amdgcn_sched_barrier(0);
       }
+      // the sums and stores, straight-line: adding an absent member's +0.0 changes no sum (the
+      // accumulator starts at +0.0 and so is never -0.0), and the output resource ends at the
+      // last vector, so a store past it is dropped
+      const __amdgpu_buffer_rsrc_t ro = uniform_rsrc(a.out + vb * 8, records);
+#pragma unroll
+      for (int i = 0; i < kVpt; i++) {
+        float acc[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) acc[e] = 0.0f;
+#pragma unroll
+        for (int q = 0; q < kMaxRows; q++) {
+#pragma unroll
+          for (int w = 0; w < 4; w++) {
+            acc[2 * w] += bf16_to_f32(x[i][q][w] & 0xffffu);
+            acc[2 * w + 1] += bf16_to_f32(x[i][q][w] >> 16);
+          }
+        }
+        u32x4 y;
+#pragma unroll
+        for (int w = 0; w < 4; w++)
+          y[w] = f32_to_bf16(acc[2 * w]) | (f32_to_bf16(acc[2 * w + 1]) << 16);
+        __builtin_amdgcn_raw_buffer_store_b128(y, ro, (i * kThreads + tid) * 16, 0,
+                                               kOutputPolicy);
+        // the store goes out now, not after the last vector's sum
+        if (EVS_REDUCE_LOAD_ORDER) __builtin_amdgcn_sched_barrier(0);
+      }
+      continue;
     } else {
 #pragma unroll
       for (int i = 0; i < kVpt; i++) {
