@@ -5,7 +5,7 @@ reference stores no golden vectors of its own. Here the oracle must still produc
 byte:
 * the gather of the reference tests' literal case (3 layouts x d in {8, 6} x bf16, f16, f32 and
   fp8) from the stored caches;
-* the scatter of the stored rows;
+* the scatter of the stored rows, in staged order and by the stored pairs;
 * the ordered sums at {16384, 3000, 2} and the order-sensitive case;
 * config C1.
 
@@ -67,6 +67,16 @@ def test_the_oracle_scatters_the_stored_rows(case):
     oracle.scatter_rows(layers, G["slots"], G["heads"], G[f"{case}_rows"], int(G["capacity"]), d,
                         int(G["block_size"]), strides_of(layers[0]), 2)
     assert np.array_equal(np.stack([mf.raw(t) for t in layers]), G[f"{case}_scattered"])
+
+
+@pytest.mark.parametrize("case", [c for c in CASES if c.endswith("bf16")])
+def test_the_oracle_scatters_the_stored_pairs(case):
+    layers = [torch.zeros_like(t) for t in tensors(case)]
+    d = int(case.rsplit("_", 2)[1][1:])
+    oracle.scatter_pairs(layers, G["pair_slots"], G["pair_rows_of"], G["heads"],
+                         G[f"{case}_rows"], int(G["capacity"]), d, int(G["block_size"]),
+                         strides_of(layers[0]), 2)
+    assert np.array_equal(np.stack([mf.raw(t) for t in layers]), G[f"{case}_paired"])
 
 
 def test_the_stored_inputs_still_come_from_the_seeds():
