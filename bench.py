@@ -884,9 +884,10 @@ def pmc_workload(ext, which="gather", launches=5):
     FETCH_SIZE and WRITE_SIZE are known to be 1 GiB each, the scale the kernel's counters are
     read against.
 
-    gather: the C2 gather. scatter: the C4 restore scatter (32 layers, 64 GiB moved).
-    reduce: the C5 local reduce, each call on another of 8 buffer sets (288 MiB in all, more
-    than the Infinity Cache holds).
+    gather: the C2 gather. scatter: the C4 restore scatter (32 layers, 64 GiB moved). pairs: the
+    same restore in cache order (scatter_pairs, the pairs sorted by slot). reduce: the C5 local
+    reduce, each call on another of 32 buffer sets (1.1 GiB in all, over 4x what the Infinity
+    Cache holds).
     """
     import torch
 
@@ -907,7 +908,7 @@ def pmc_workload(ext, which="gather", launches=5):
             ext.gather_rows(ptrs, s, heads, out.data_ptr(), n, D, BS, strides, 2)
         algo = 2 * L * H * n * 2 * D * 2
         del layers, out
-    elif which == "scatter":
+    elif which in ("scatter", "pairs"):
         L, NB, BS, H, D = 32, 16384, 16, 8, 128
         n = NB * BS
         # the counters count bytes, whatever they hold: the rows are left uninitialised
@@ -919,8 +920,17 @@ def pmc_workload(ext, which="gather", launches=5):
         s = torch.from_numpy(slots).to(dev)
         heads = torch.arange(H, dtype=torch.long, device=dev)
         strides = layout_strides(caches[0])
+        if which == "pairs":
+            from everserve_amd.state.restore import destination_order
+
+            o_slots, o_rows = destination_order(slots, block_size=BS)
+            os_dev, or_dev = torch.from_numpy(o_slots).to(dev), torch.from_numpy(o_rows).to(dev)
         for _ in range(launches):
-            ext.scatter_rows(ptrs, s, heads, rows.data_ptr(), n, D, BS, strides, 2)
+            if which == "pairs":
+                ext.scatter_pairs(ptrs, os_dev, or_dev, heads, rows.data_ptr(), n, D, BS, strides,
+                                  2)
+            else:
+                ext.scatter_rows(ptrs, s, heads, rows.data_ptr(), n, D, BS, strides, 2)
         algo = 2 * L * H * n * 2 * D * 2
         del rows, caches
     elif which == "reduce":
@@ -965,7 +975,7 @@ def main(argv=None):
                     help="only the host copies of the path beside plain copies, for a "
                          "rocprofv3 memory-copy trace")
     ap.add_argument("--pmc", nargs="?", const="gather", default=None,
-                    choices=("gather", "scatter", "reduce"),
+                    choices=("gather", "scatter", "pairs", "reduce"),
                     help="only a counter run's workload: 5 calls of the named kernel (default "
                          "gather), then 5 calibration copies")
     a = ap.parse_args(argv)
