@@ -474,10 +474,24 @@ def bench_c4(ext, steps, warmup):
     ext.gather_rows(ptrs[:4], s, heads, back.data_ptr(), n, D, BS, strides, 2)
     torch.cuda.synchronize()
     ok_o = bool(torch.equal(back.view(torch.int16), rows[:4].view(torch.int16)))
+
+    # the same with the pairs ordered on the device (evs_order_pairs), the sort inside the timing
+    def ordered_on_device():
+        o_s, o_r = ext.order_pairs(s, NB * BS)
+        ext.scatter_pairs(ptrs, o_s, o_r, heads, rows.data_ptr(), n, D, BS, strides, 2)
+
+    for t in caches[:4]:
+        t.zero_()
+    per_d, _ = time_launches(ordered_on_device, steps, warmup, stream)
+    ext.gather_rows(ptrs[:4], s, heads, back.data_ptr(), n, D, BS, strides, 2)
+    torch.cuda.synchronize()
+    ok_d = bool(torch.equal(back.view(torch.int16), rows[:4].view(torch.int16)))
+    per_sort, _ = time_launches(lambda: ext.order_pairs(s, NB * BS), steps, warmup, stream)
     del rows, caches, back
     torch.cuda.empty_cache()
     ms = sum(per) / len(per)
     ms_o = sum(per_o) / len(per_o)
+    ms_d = sum(per_d) / len(per_d)
     return {
         "config": "C4 restore: [32,8,262144,2,128] bf16 rows into a fresh 16384-block cache, "
                   "random-permutation block table (64 seqs x 4096 tokens)",
@@ -493,6 +507,15 @@ def bench_c4(ext, steps, warmup):
             "scatter_frac_of_8tbs": round(2 * payload / ms_o / 1e6 / PEAK_HBM_GBS, 4),
             "order_host_ms": round(order_ms, 2),
             "round_trip_equal_first_4_layers": ok_o,
+        },
+        "ordered_on_device": {
+            "how": "order_pairs (a radix sort of the slot ids on the device) then scatter_pairs, "
+                   "both inside each timed launch",
+            "ms": round(ms_d, 3),
+            "gbs": round(2 * payload / ms_d / 1e6, 1),
+            "frac_of_8tbs": round(2 * payload / ms_d / 1e6 / PEAK_HBM_GBS, 4),
+            "sort_ms": round(sum(per_sort) / len(per_sort), 4),
+            "round_trip_equal_first_4_layers": ok_d,
         },
     }
 

@@ -28,7 +28,8 @@ CSRC = PACKAGE / "csrc"
 INCLUDE = ROOT / "include"
 LIBRARY = "libeverserve_mi355x.so"
 STAMP = "stamp.json"
-SOURCES = ("rows.hip", "reduce.hip", "slot.hip", "host_rows.hip", "store.hip", "runtime.hip")
+SOURCES = ("rows.hip", "order.hip", "reduce.hip", "slot.hip", "host_rows.hip", "store.hip",
+           "runtime.hip")
 HEADERS = ("common.hpp",)
 PUBLIC_HEADERS = ("everserve_mi355x.h",)
 DEFAULT_ARCHS = "gfx950"

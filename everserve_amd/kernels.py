@@ -148,6 +148,8 @@ _SIGNATURES: tuple[tuple[str, object, tuple], ...] = (
     ("evs_scatter_rows", _I32, (_P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _P, _I64, _P)),
     ("evs_scatter_pairs", _I32,
      (_P, _I64, _P, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _P, _I64, _P)),
+    ("evs_order_pairs_workspace", _I32, (_I64, _I32, _P)),
+    ("evs_order_pairs", _I32, (_P, _I64, _I32, _P, _P, _P, _I64, _P)),
     ("evs_local_reduce", _I32, (_P, _P, _P, _P, _I64, ctypes.c_uint64, _I64, _P, _P, _P)),
     ("evs_slot_all_reduce", _I32,
      (_P, _P, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I32, _I64, _P)),
@@ -387,6 +389,34 @@ class Kernels:
                     _stream_of(slots.device),
                 )
             )
+
+    def order_pairs(self, slots, num_slots: int):
+        """``(slots_sorted, rows_of)`` for :meth:`scatter_pairs`, ordered on the device.
+
+        ``slots`` (int64, on the device) are the cache slots of staged rows 0..n-1 and
+        ``num_slots`` the cache's slot count, which fixes the key bits compared. The result is
+        ``slots`` by increasing slot and the staged row of each (stable). A padding slot
+        (negative) is kept and lands anywhere; the pair scatter skips it. The workspace and the
+        outputs are allocated here, on the current stream of the slots' device, which the sort
+        is enqueued on.
+        """
+        import torch
+
+        sp = _device_ptr(slots, "order_pairs: slots", torch.long)
+        n = slots.numel()
+        bits = max(1, (int(num_slots) - 1).bit_length())
+        need = ctypes.c_int64()
+        with torch.cuda.device(slots.device):
+            self._check(self._lib.evs_order_pairs_workspace(n, bits, ctypes.byref(need)))
+            work = torch.empty(max(1, need.value), dtype=torch.uint8, device=slots.device)
+            out_slots = torch.empty_like(slots)
+            out_rows = torch.empty_like(slots)
+            self._check(
+                self._lib.evs_order_pairs(sp, n, bits, out_slots.data_ptr(), out_rows.data_ptr(),
+                                          work.data_ptr(), work.numel(),
+                                          _stream_of(slots.device))
+            )
+        return out_slots, out_rows
 
     def copy_rows_async(self, dst_ptr: int, src_ptr: int, groups: int, bytes_: int, pitch: int,
                         device=None) -> None:

@@ -115,6 +115,19 @@ int evs_scatter_pairs(const int64_t* layer_ptrs, int64_t num_layers, const int64
                       int64_t block_size, const int64_t* strides, int64_t elem_size,
                       void* stream);
 
+/* The pairs for evs_scatter_pairs in slot order, on the device, for a caller whose slot list is
+ * in HBM: slots_out[i] = slots[rows_out[i]], by increasing slot, where rows_out is a permutation
+ * of 0..num_pairs-1 (stable: equal slots keep their listed order). Only the low key_bits bits of
+ * a slot id are compared (1..64; at least the bits of the cache's largest slot id); a negative
+ * slot id (padding) lands wherever its low bits put it, and evs_scatter_pairs skips it.
+ * `workspace` is device memory of at least evs_order_pairs_workspace(num_pairs, key_bits) bytes,
+ * 256-byte aligned, owned by the caller; the call allocates nothing and does not synchronise.
+ * num_pairs < 2^31. No counterpart in the reference: it orders the restore's writes (see
+ * evs_scatter_pairs); the host-side equivalent is everserve_amd.state.restore.destination_order. */
+int evs_order_pairs_workspace(int64_t num_pairs, int key_bits, int64_t* bytes);
+int evs_order_pairs(const int64_t* slots, int64_t num_pairs, int key_bits, int64_t* slots_out,
+                    int64_t* rows_out, void* workspace, int64_t workspace_bytes, void* stream);
+
 /* The reduction stage of the failure-detecting all-reduce over member buffers already in this
  * GPU's HBM (the local stage of core/csrc/slot.cu:118-224):
  *
