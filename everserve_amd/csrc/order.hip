@@ -4,7 +4,8 @@
 // the low key_bits bits of the slot ids (the cache's slot count fixes how many matter: 18 for
 // 262,144 slots). The sort is stable, so equal slots keep their listed order. Everything it needs
 // beyond its inputs and outputs lives in a workspace the caller allocates: the row numbers
-// 0..n-1, then rocPRIM's temporary storage.
+// 0..n-1, then rocPRIM's temporary storage. rocPRIM clears its counters there with
+// hipMemsetAsync, so this call is not one to capture in a HIP graph.
 
 #include <rocprim/device/device_radix_sort.hpp>
 

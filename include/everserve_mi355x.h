@@ -122,7 +122,8 @@ int evs_scatter_pairs(const int64_t* layer_ptrs, int64_t num_layers, const int64
  * slot id (padding) lands wherever its low bits put it, and evs_scatter_pairs skips it.
  * `workspace` is device memory of at least evs_order_pairs_workspace(num_pairs, key_bits) bytes,
  * 256-byte aligned, owned by the caller; the call allocates nothing and does not synchronise.
- * num_pairs < 2^31. No counterpart in the reference: it orders the restore's writes (see
+ * The sort clears its own counters in the workspace with hipMemsetAsync, so keep this call out
+ * of captured HIP graphs. num_pairs < 2^31. No counterpart in the reference: it orders the restore's writes (see
  * evs_scatter_pairs); the host-side equivalent is everserve_amd.state.restore.destination_order. */
 int evs_order_pairs_workspace(int64_t num_pairs, int key_bits, int64_t* bytes);
 int evs_order_pairs(const int64_t* slots, int64_t num_pairs, int key_bits, int64_t* slots_out,
