@@ -63,7 +63,8 @@ extern "C" int evs_order_pairs(const int64_t* slots, int64_t num_pairs, int key_
   EVS_REQUIRE(slots != nullptr && slots_out != nullptr && rows_out != nullptr &&
                   workspace != nullptr,
               "evs_order_pairs: null pointer");
-  EVS_REQUIRE(workspace_bytes >= need, "evs_order_pairs: the workspace holds %lld bytes, %lld needed",
+  EVS_REQUIRE(workspace_bytes >= need,
+              "evs_order_pairs: the workspace holds %lld bytes, %lld needed",
               static_cast<long long>(workspace_bytes), static_cast<long long>(need));
   EVS_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & (evs::kAlign - 1)) == 0,
               "evs_order_pairs: the workspace must be %lld-byte aligned",
@@ -78,7 +79,8 @@ extern "C" int evs_order_pairs(const int64_t* slots, int64_t num_pairs, int key_
   EVS_LAUNCHED("evs_order_pairs");
   // the slot ids are compared as unsigned on their low key_bits bits: a padding id (negative)
   // lands wherever those bits put it, and the pair scatter skips it
-  EVS_HIP(rocprim::radix_sort_pairs(sort_tmp, sort_bytes, reinterpret_cast<const uint64_t*>(slots),
+  EVS_HIP(rocprim::radix_sort_pairs(sort_tmp, sort_bytes,
+                                    reinterpret_cast<const uint64_t*>(slots),
                                     reinterpret_cast<uint64_t*>(slots_out),
                                     static_cast<const int64_t*>(rows), rows_out,
                                     static_cast<uint32_t>(num_pairs), 0u,
