@@ -24,7 +24,8 @@
 // words in cache order and issuing a tile's loads before its slot ids are read (both slower);
 // fewer workgroups per CU (unused LDS as a cap), which speeds a plain copy up by 8 % at 8 KiB per
 // workgroup but slows these kernels, whose index prologue needs every resident workgroup to hide
-// its latency.
+// its latency; each wave reading its own rows' ids with scalar loads, no LDS and no barrier
+// (2 % slower: the per-lane choice among the wave's rows costs more than the barrier).
 
 #include "common.hpp"
 
