@@ -24,10 +24,13 @@ void clear_error();
     }                                 \
   } while (0)
 
+// A failed call's error is reported here, and read out of HIP's per-thread last error, so that a
+// later launch check (EVS_LAUNCHED) does not report it again as its own.
 #define EVS_HIP(call)                                                                     \
   do {                                                                                    \
     hipError_t evs_rc_ = (call);                                                          \
     if (evs_rc_ != hipSuccess) {                                                          \
+      (void)hipGetLastError();                                                            \
       ::evs::set_error("%s failed: %s (%d)", #call, hipGetErrorString(evs_rc_),          \
                        static_cast<int>(evs_rc_));                                        \
       return EVS_EHIP;                                                                    \

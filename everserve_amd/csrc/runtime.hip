@@ -77,6 +77,7 @@ extern "C" int evs_host_register_mapped(void* ptr, int64_t bytes, void** device_
   void* dev = nullptr;
   hipError_t rc = hipHostGetDevicePointer(&dev, ptr, 0);
   if (rc != hipSuccess) {
+    (void)hipGetLastError();
     (void)hipHostUnregister(ptr);
     evs::set_error("hipHostGetDevicePointer failed: %s (%d)", hipGetErrorString(rc),
                    static_cast<int>(rc));
@@ -103,6 +104,7 @@ extern "C" int evs_host_alloc_mapped(int64_t bytes, void** host_ptr, void** devi
   void* dev = nullptr;
   hipError_t rc = hipHostGetDevicePointer(&dev, h, 0);
   if (rc != hipSuccess) {
+    (void)hipGetLastError();
     (void)hipHostFree(h);
     evs::set_error("hipHostGetDevicePointer failed: %s (%d)", hipGetErrorString(rc),
                    static_cast<int>(rc));
@@ -126,6 +128,7 @@ extern "C" int evs_device_alloc(int64_t bytes, void** ptr) {
   EVS_HIP(hipMalloc(&p, static_cast<size_t>(bytes)));
   hipError_t rc = hipMemset(p, 0, static_cast<size_t>(bytes));
   if (rc != hipSuccess) {
+    (void)hipGetLastError();
     (void)hipFree(p);
     evs::set_error("hipMemset failed: %s (%d)", hipGetErrorString(rc), static_cast<int>(rc));
     return EVS_EHIP;
