@@ -205,6 +205,39 @@ def test_c2_full_size_round_trip(ext):
         assert torch.equal(out[li].view(torch.int16), want.view(torch.int16)), li
 
 
+@pytest.mark.parametrize("layout", ["blocks_first", "combined"])
+def test_c2_shape_round_trip_in_the_other_layouts(ext, layout):
+    """The C2 per-layer shape in the other two paged layouts, four layers (512 MiB each): the
+    gathered rows equal the layout's torch indexing (PagedKV.rows_of_heads, on the device), and
+    scattered into zeroed caches they restore exactly the gathered blocks, nothing else."""
+    from everserve_amd.state.kvcopy import PagedKV
+
+    L, NB, BS, H, D = 4, 8192, 16, 8, 128
+    shape = {"blocks_first": (NB, 2, BS, H, D), "combined": (NB, H, BS, 2 * D)}[layout]
+    g = torch.Generator(device="cuda").manual_seed(5)
+    layers = [torch.empty(shape, dtype=torch.bfloat16, device="cuda").normal_(generator=g)
+              for _ in range(L)]
+    blocks, slots = block_table(NB, 1024, BS, seed=2)
+    n = len(slots)
+    s = torch.from_numpy(slots).cuda()
+    heads = torch.arange(H, dtype=torch.long, device="cuda")
+    strides = list(strides_of(layers[0]))
+    out = torch.empty((L, H, n, 2, D), dtype=torch.bfloat16, device="cuda")
+    ext.gather_rows(ptrs(layers), s, heads, out.data_ptr(), n, D, BS, strides, 2)
+    fresh = [torch.zeros_like(t) for t in layers]
+    ext.scatter_rows(ptrs(fresh), s, heads, out.data_ptr(), n, D, BS, strides, 2)
+    torch.cuda.synchronize()
+    paged = PagedKV.of(layers[0])
+    b = torch.from_numpy(blocks).cuda()
+    keep = torch.ones(NB, dtype=torch.bool, device="cuda")
+    keep[b] = False
+    for li, (orig, back) in enumerate(zip(layers, fresh)):
+        want = paged.rows_of_heads(orig, s, heads)  # [H, n, 2, D]
+        assert torch.equal(out[li].view(torch.int16), want.contiguous().view(torch.int16)), li
+        assert torch.equal(orig[b].view(torch.int16), back[b].view(torch.int16)), li
+        assert not back[keep].view(torch.int16).any(), li
+
+
 def test_c3_fp8_share_gather_and_copy_to_pinned_memory(ext):
     """C3: 80 layers of a one-head fp8 e4m3 cache, 2048 blocks gathered and copied to pinned host
     memory; the bytes equal the oracle's on a layer subset and the device staging on all."""
