@@ -363,9 +363,10 @@ def bench_store_commit(ext, steps, warmup):
 
 # ------------------------------------------------------------------------------ C3 fp8 + D2H
 def bench_c3(ext, steps, warmup):
-    import torch
+    import ctypes
 
     import numpy as np
+    import torch
 
     L, NB, BS, H, D = 80, 8192, 16, 1, 128
     dev = torch.device("cuda", 0)
@@ -406,6 +407,22 @@ def bench_c3(ext, steps, warmup):
     torch.cuda.synchronize()
     ok = bool(torch.equal(host[7, 0, :BS].view(-1).cpu(),
                           staging[7, 0, :BS].view(-1).cpu()))
+    # the reference's way: the gather writes the rows straight into host memory mapped for the
+    # device (here hipHostMalloc'd, since registering existing memory is refused on this pool)
+    host_ptr, mapped_ptr = ext.host_alloc_mapped(payload)
+    try:
+        def zero_copy():
+            ext.gather_rows(ptrs, s, heads, mapped_ptr, n, D, BS, strides, 1)
+
+        z_per, _ = time_launches(zero_copy, max(3, steps // 4), 2, stream)
+        torch.cuda.synchronize()
+        mapped = np.ctypeslib.as_array((ctypes.c_uint8 * payload).from_address(host_ptr))
+        ok_zero_copy = bool(np.array_equal(mapped[:1 << 20], staging.view(-1)[:1 << 20].cpu().numpy())
+                            and np.array_equal(mapped[-(1 << 20):],
+                                               staging.view(-1)[-(1 << 20):].cpu().numpy()))
+    finally:
+        ext.host_free(host_ptr)
+    z_ms = sum(z_per) / len(z_per)
     del layers, staging
     torch.cuda.empty_cache()
     plain = pinned_copy_gbs(payload, to_host=True)
@@ -422,6 +439,9 @@ def bench_c3(ext, steps, warmup):
         "d2h_plain_memcpy_gbs": round(plain, 2),
         "d2h_frac_of_plain_memcpy": round(payload / c_ms / 1e6 / plain, 4),
         "gather_plus_d2h_ms": round(b_ms, 3),
+        "zero_copy_gather_ms": round(z_ms, 3),
+        "zero_copy_gather_gbs": round(payload / z_ms / 1e6, 2),
+        "zero_copy_bytes_equal": ok_zero_copy,
         "scales": "80 fp32 per-layer scales U(0.01, 0.1) copied beside the rows (not inside "
                   "them); values fp8(N(0,1) / scale)",
         "bytes_equal_after_d2h": ok,

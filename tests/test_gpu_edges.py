@@ -146,6 +146,28 @@ def test_256_head_slots_in_one_call_and_257_refused(ext):
         assert live and all(np.array_equal(bits(a), bits(b)) for a, b in zip(dst, ref))
 
 
+@pytest.mark.parametrize("d", [8, 6])
+def test_the_gather_writes_straight_into_mapped_host_memory(ext, d):
+    """Zero-copy, as the reference's staging does: out is host memory mapped for the device."""
+    import ctypes
+
+    layers = caches("kv_first", d, torch.bfloat16, n_layers=L, nb=NB, h=H, seed=44)
+    slots, heads, cap = ragged_slots(61, 44), [1, 2], 64
+    want = np.full((L, len(heads), cap, 2, d), SENTINEL, dtype=np.uint16)
+    oracle.gather_rows(layers, slots, heads, cap, d, BS, strides_of(layers[0]), 2, out=want)
+    gpu = [t.cuda() for t in layers]
+    host, mapped = ext.host_alloc_mapped(want.nbytes)
+    try:
+        h = np.ctypeslib.as_array((ctypes.c_uint16 * want.size).from_address(host))
+        h[:] = SENTINEL
+        ext.gather_rows(ptrs(gpu), dev_long(slots), dev_long(heads), mapped, cap, d, BS,
+                        list(strides_of(gpu[0])), 2)
+        torch.cuda.synchronize()
+        assert np.array_equal(h.reshape(want.shape), want)
+    finally:
+        ext.host_free(host)
+
+
 def test_fp8_e5m2_moves_as_raw_bytes(ext):
     layers = caches("blocks_first", 8, torch.float8_e5m2, n_layers=L, nb=NB, h=H, seed=4)
     slots = ragged_slots(33, 4)
