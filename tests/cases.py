@@ -77,3 +77,72 @@ def brute_gather(layers, slots, heads, capacity: int) -> np.ndarray:
                         row = a[b, head, o, k * d:(k + 1) * d]
                     out[li, hi, ti, k] = row
     return out
+
+
+def random_case(seed: int) -> dict:
+    """One seeded draw over what a caller may pass: any of the three layouts, element type, head
+    dim (16-byte rows and not), block size (powers of two and not), head count, a held-head list
+    in any order, 1 to 200 slots (about one in ten padding), spare capacity, and the cache as a
+    contiguous tensor, a head-sliced view of a wider one, or (combined) the reference's permuted
+    [nb, bs, h, 2d] build. ``base`` holds the CPU tensors the caches are views of; ``view`` turns
+    one (or its device copy) into the cache, so that a device cache keeps the same strides."""
+    rng = np.random.default_rng(seed)
+    layout = LAYOUTS[int(rng.integers(len(LAYOUTS)))]
+    dtype = DTYPES[int(rng.integers(len(DTYPES)))]
+    d = int(rng.choice([2, 4, 6, 8, 16, 24, 64, 128]))
+    bs = int(rng.choice([1, 2, 3, 4, 5, 7, 16]))
+    h = int(rng.integers(1, 10))
+    nb = int(rng.integers(1, 41))
+    n_layers = int(rng.integers(1, 4))
+    heads = rng.permutation(h)[:int(rng.integers(1, h + 1))].tolist()
+    n = int(rng.integers(1, min(nb * bs, 200) + 1))
+    slots = rng.choice(nb * bs, size=n, replace=False).astype(np.int64)
+    slots[rng.random(n) < 0.1] = -1
+    kind = rng.choice(["contiguous", "head_slice", "permuted"] if layout == "combined"
+                      else ["contiguous", "head_slice"])
+    g = torch.Generator().manual_seed(seed)
+    wide = h + 1 if kind == "head_slice" else h
+    if kind == "permuted":
+        shape = (nb, bs, h, 2 * d)
+
+        def view(t):
+            return t.permute(0, 2, 1, 3)
+    else:
+        shape = cache_shape(layout, nb, bs, wide, d)
+        hdim = 1 if layout == "combined" else 3
+
+        def view(t):
+            return t.narrow(hdim, wide - h, h)
+    base = []
+    for _ in range(n_layers):
+        x = torch.randn(shape, generator=g)
+        if dtype in (torch.float8_e4m3fn, torch.float8_e5m2):
+            x = (x / 0.05).clamp(-448, 448)
+        base.append(x.to(dtype))
+    return dict(seed=seed, layout=layout, dtype=dtype, d=d, bs=bs, h=h, nb=nb, heads=heads,
+                slots=slots, cap=n + int(rng.integers(0, 5)), kind=str(kind), base=base,
+                view=view, rng=rng)
+
+
+def brute_scatter(layers, slots, heads, rows) -> list[np.ndarray]:
+    """The scatter by its definition per layout, on raw-bit copies of ``layers``: for each listed
+    slot s >= 0 at position t, the K (k=0) or V (k=1) half-row of head slot heads[h] at s becomes
+    rows[l, h, t, k]; everything else keeps its bits. Returns the new bits, one array a layer."""
+    layout, _, bs, d = oracle.recognise(layers[0].shape)
+    out = []
+    for li, t in enumerate(layers):
+        a = bits(t).copy()
+        for hi, head in enumerate(heads):
+            for ti, s in enumerate(slots):
+                if s < 0:
+                    continue
+                b, o = divmod(int(s), bs)
+                for k in range(2):
+                    if layout == "kv_first":
+                        a[k, b, o, head, :] = rows[li, hi, ti, k]
+                    elif layout == "blocks_first":
+                        a[b, k, o, head, :] = rows[li, hi, ti, k]
+                    else:
+                        a[b, head, o, k * d:(k + 1) * d] = rows[li, hi, ti, k]
+        out.append(a)
+    return out
