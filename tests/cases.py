@@ -146,3 +146,31 @@ def brute_scatter(layers, slots, heads, rows) -> list[np.ndarray]:
                         a[b, head, o, k * d:(k + 1) * d] = rows[li, hi, ti, k]
         out.append(a)
     return out
+
+
+SPECIAL_N = 1 << 16
+
+
+def special_members() -> dict[int, np.ndarray]:
+    """bf16 members (raw bits) that reach the sum's special cases, SPECIAL_N elements each.
+
+    0: every bf16 bit pattern once: zeros of both signs, subnormals, the largest finite values,
+       infinities and NaNs of both signs;
+    1: the same patterns rotated, so that inf meets -inf, NaN meets numbers and large values of
+       one sign meet (an fp32 sum past bf16's range rounds to infinity);
+    2: uniform random bits;
+    3: half a bf16 unit in the last place of member 0's value, with its sign (zero where that
+       is not a normal bf16), so that member 0 + member 3 is an exact tie for the rounding.
+    """
+    every = np.arange(SPECIAL_N, dtype=np.uint32).astype(np.uint16)
+    expo = (every.astype(np.int32) >> 7) & 0xFF
+    half_ulp = np.where((expo > 8) & (expo < 255),
+                        ((expo - 8) << 7) | (every.astype(np.int32) & 0x8000), 0).astype(np.uint16)
+    rng = np.random.default_rng(77)
+    return {0: every, 1: np.roll(every, 40961),
+            2: rng.integers(0, 1 << 16, size=SPECIAL_N, dtype=np.uint16), 3: half_ulp}
+
+
+def bf16_tensor(raw: np.ndarray) -> torch.Tensor:
+    """A CPU bf16 tensor holding the raw bits ``raw`` (uint16)."""
+    return torch.from_numpy(np.ascontiguousarray(raw).view(np.int16)).view(torch.bfloat16)

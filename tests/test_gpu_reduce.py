@@ -19,7 +19,7 @@ import torch
 
 import oracle
 from everserve_amd.kernels import REDUCE_STATE_WORDS
-from tests.cases import bits
+from tests.cases import bf16_tensor, bits, special_members
 
 pytestmark = pytest.mark.gpu
 
@@ -215,3 +215,18 @@ def test_a_captured_reduction_replays_like_eager_calls(ext):
         assert np.array_equal(bits(m.out), want), i
         assert m.status() == (5, 0, 0)
         assert not m.state[1:].any()
+
+
+@pytest.mark.parametrize("order", [[0], [0, 1], [1, 0, 2], [0, 3], [3, 0], [2, 0, 1, 3]])
+def test_special_values_round_as_the_oracle_does(ext, order):
+    """Every bf16 pattern (signed zeros, subnormals, the largest values, infinities, NaNs), sums
+    that overflow, inf meeting -inf, and exact ties: the kernel's fp32 adds keep subnormals and
+    its rounding matches the oracle's bit for bit (tests/cases.py:special_members)."""
+    members = special_members()
+    inputs = {r: bf16_tensor(members[r]) for r in order}
+    m = Members(inputs, order)
+    m.publish(epoch=1)
+    ext.local_reduce(m.bufs, m.flags, m.order, m.out, 1, 10**9, 0, m.state)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(m.out), oracle.member_sum([members[r] for r in order]))
+    assert m.status() == (1, 0, 0)

@@ -18,7 +18,7 @@ import pytest
 import torch
 
 import oracle
-from tests.cases import bits
+from tests.cases import bf16_tensor, bits, special_members
 
 pytestmark = pytest.mark.gpu
 
@@ -259,5 +259,25 @@ def test_bad_arguments_are_refused(ext):
             ext.slot_all_reduce(x, x, reg.bufs, reg.ctrl_dev, order, seqs, 8, MAXN, 1, False)
         with pytest.raises(KernelError, match="too few counters"):
             ext.slot_all_reduce(x, x, reg.bufs, reg.ctrl_dev, order, seqs[:5], 0, MAXN, 1, False)
+    finally:
+        reg.close()
+
+
+@pytest.mark.parametrize("push", [False, True])
+def test_special_values_round_as_the_oracle_does(ext, push):
+    """The slot collective over every bf16 pattern, overflowing sums and exact ties
+    (tests/cases.py:special_members): the same bits as the oracle's ordered sum."""
+    members = special_members()
+    rows = [0, 1, 2]
+    xs = {0: bf16_tensor(members[0]), 1: bf16_tensor(members[1]), 2: bf16_tensor(members[3])}
+    reg = Region(ext, push, rows)
+    try:
+        order, seqs = reg.member(rows)
+        for r in (1, 2):
+            reg.stage(0, r, xs[r], seq=1)
+        out = reduce(ext, reg, 0, order, seqs, xs[0], 1)
+        torch.cuda.synchronize()
+        want = oracle.member_sum([members[0], members[1], members[3]])
+        assert np.array_equal(bits(out), want)
     finally:
         reg.close()

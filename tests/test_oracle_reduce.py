@@ -17,6 +17,7 @@ import pytest
 import torch
 
 import oracle
+from tests.cases import bf16_tensor, special_members
 
 
 def bf16_bits(t: torch.Tensor) -> np.ndarray:
@@ -177,3 +178,26 @@ def test_the_cpu_path_member_sum_is_the_oracles(n):
     xs = [member_input(r, n) for r in range(8)]
     got = bf16_bits(cpu_path.member_sum(xs))
     assert np.array_equal(got, oracle.member_sum([bf16_bits(x) for x in xs]))
+
+
+SPECIAL_ORDERS = [[0], [0, 1], [1, 0, 2], [0, 3], [3, 0], [2, 0, 1, 3]]
+
+
+@pytest.mark.parametrize("order", SPECIAL_ORDERS)
+def test_special_values_sum_as_torch_does(order):
+    """Every bf16 pattern through the sum: torch's fp32 adds and bf16 rounding give the same bits
+    except at NaN, where the oracle keeps c10's 0x7FC0 (see the rounding test above)."""
+    members = special_members()
+    got = oracle.member_sum([members[r] for r in order])
+    want = bf16_bits(torch_sum([bf16_tensor(members[r]) for r in order]))
+    nan = np.isnan(oracle.bf16_to_float(want))
+    assert np.array_equal(got[~nan], want[~nan])
+    assert (got[nan] == 0x7FC0).all()
+    if order == [0, 3]:
+        # the ties: half an ulp added to an odd mantissa rounds up, to an even one stays
+        v = members[0]
+        tie = (members[3] != 0) & ((v & 0x7F80) != 0x7F80)
+        odd = (v & 1) == 1
+        assert tie.sum() > 50_000
+        assert np.array_equal(got[tie & ~odd], v[tie & ~odd])
+        assert np.array_equal(got[tie & odd], v[tie & odd] + 1)
