@@ -572,34 +572,47 @@ def bench_restore_host(ext, steps, warmup):
         written = [(0, n)]
         caches = [torch.zeros((2, NB, BS, H, D), dtype=torch.bfloat16, device=dev) for _ in range(L)]
         head_map = {h: (h + 3) % H for h in range(H)}
-        restorer = Restorer(ext, caches)
-        tables = [Table.open(t, p, written) for t, p in paths.items()]
-        restorer.restore(tables[:2], head_map)  # warm: page in, pinned buffers touched
-        t0 = time.perf_counter()
-        rows = restorer.restore(tables, head_map)
-        ours_s = time.perf_counter() - t0
+        # Four restores, each mapping the tables afresh inside its timing as the reference's
+        # does. The first is cold and includes building the Restorer (its pinned and device
+        # buffers); the other three are the steady state, reported by their median.
+        ours = []
+        restorer = None
+        for _ in range(4):
+            t0 = time.perf_counter()
+            if restorer is None:
+                restorer = Restorer(ext, caches)
+            tables = [Table.open(t, p, written) for t, p in paths.items()]
+            rows = restorer.restore(tables, head_map)
+            ours.append(time.perf_counter() - t0)
+            del tables
+        ours_s = sorted(ours[1:])[1]
         payload = rows * row_bytes
         # check: layer 2's new head slot of theirs 5, slot ids 0..15
         got = caches[2][:, 0, :, head_map[5]].permute(1, 0, 2).contiguous()  # [16, 2, D]
         want = torch.from_numpy(base[: 16 * 2 * D].view(np.int16).reshape(16, 2, D).copy())
         ok = bool(torch.equal(got.view(torch.int16).cpu(), want))
 
-        # the reference's procedure on the same files (torch's gather on one host thread)
+        # the reference's procedure on the same files: torch's index_select (on torch's
+        # intra-op threads) into pinned memory allocated per table, then write_rows
         paged = PagedKV.of(caches[0])
         idx = torch.cat([torch.arange(s, s + c, dtype=torch.long) for s, c in written])
         idx_dev = idx.to(dev)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for table, path in paths.items():
-            layer, head = divmod(table, 1000)
-            src = torch.from_file(path, shared=True, size=n * 2 * D, dtype=torch.bfloat16)
-            src = src.view(n, 2, D)
-            pinned = torch.empty((idx.numel(), 2, D), dtype=torch.bfloat16, pin_memory=True)
-            torch.index_select(src, 0, idx, out=pinned)
-            on_device = pinned.to(dev, non_blocking=True)
-            paged.write_rows(caches[layer], idx_dev, head_map[head], on_device.transpose(0, 1))
-        torch.cuda.synchronize()
-        ref_s = time.perf_counter() - t0
+        ref = []
+        for _ in range(4):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for table, path in paths.items():
+                layer, head = divmod(table, 1000)
+                src = torch.from_file(path, shared=True, size=n * 2 * D, dtype=torch.bfloat16)
+                src = src.view(n, 2, D)
+                pinned = torch.empty((idx.numel(), 2, D), dtype=torch.bfloat16, pin_memory=True)
+                torch.index_select(src, 0, idx, out=pinned)
+                on_device = pinned.to(dev, non_blocking=True)
+                paged.write_rows(caches[layer], idx_dev, head_map[head],
+                                 on_device.transpose(0, 1))
+            torch.cuda.synchronize()
+            ref.append(time.perf_counter() - t0)
+        ref_s = sorted(ref[1:])[1]
     finally:
         shutil.rmtree(tmp, ignore_errors=True)
     del caches
@@ -610,11 +623,19 @@ def bench_restore_host(ext, steps, warmup):
                   f"each, every slot written) from /dev/shm files into a fresh 16384-block cache "
                   f"at other head slots",
         "payload_bytes": payload,
+        "timing": "4 restores each, every one mapping the tables afresh inside its timing: the "
+                  "first cold (ours including building the Restorer), the steady state the "
+                  "median of the other 3",
         "ours_s": round(ours_s, 3),
         "ours_gbs": round(payload / ours_s / 1e9, 2),
         "reference_procedure_s": round(ref_s, 3),
         "reference_procedure_gbs": round(payload / ref_s / 1e9, 2),
         "speedup": round(ref_s / ours_s, 2),
+        "first_restore": {
+            "ours_gbs": round(payload / ours[0] / 1e9, 2),
+            "reference_procedure_gbs": round(payload / ref[0] / 1e9, 2),
+            "speedup": round(ref[0] / ours[0], 2),
+        },
         "h2d_plain_memcpy_gbs": round(plain, 2),
         "frac_of_plain_h2d": round(payload / ours_s / 1e9 / plain, 4),
         "rows_check": ok,

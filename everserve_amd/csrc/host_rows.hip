@@ -10,10 +10,47 @@
 
 #include "common.hpp"
 
+// 1: the rows are written with nontemporal stores. A plain store first reads every line it
+// writes into the cache (a third stream of host memory traffic beside the table's reads and the
+// DMA engine's), and leaves the pinned lines dirty in the copying core's cache.
+#ifndef EVS_HOST_NT_STORES
+#define EVS_HOST_NT_STORES 1
+#endif
+
 namespace evs {
 namespace {
 
 constexpr int64_t kMinBytesPerThread = int64_t{4} << 20;  // below this a thread costs more than it copies
+
+typedef long long v2i64 __attribute__((ext_vector_type(2)));
+
+// memcpy with 16-byte nontemporal stores where dst is 16-byte aligned; plain copies for the
+// unaligned head and the tail.
+void stream_copy(char* dst, const char* src, size_t bytes) {
+  size_t head = (16 - (reinterpret_cast<uintptr_t>(dst) & 15)) & 15;
+  if (head > bytes) head = bytes;
+  std::memcpy(dst, src, head);
+  size_t i = head;
+  for (; i + 64 <= bytes; i += 64) {
+    v2i64 w[4];
+    std::memcpy(w, src + i, 64);
+    for (int k = 0; k < 4; k++)
+      __builtin_nontemporal_store(w[k], reinterpret_cast<v2i64*>(dst + i) + k);
+  }
+  for (; i + 16 <= bytes; i += 16) {
+    v2i64 w;
+    std::memcpy(&w, src + i, 16);
+    __builtin_nontemporal_store(w, reinterpret_cast<v2i64*>(dst + i));
+  }
+  std::memcpy(dst + i, src + i, bytes - i);
+}
+
+void copy_bytes(char* dst, const char* src, size_t bytes) {
+  if (EVS_HOST_NT_STORES)
+    stream_copy(dst, src, bytes);
+  else
+    std::memcpy(dst, src, bytes);
+}
 
 // Copy output rows [r0, r1) of the concatenated ranges.
 void copy_rows(const char* src, int64_t row_bytes, const int64_t* starts, const int64_t* counts,
@@ -29,10 +66,12 @@ void copy_rows(const char* src, int64_t row_bytes, const int64_t* starts, const 
     const int64_t in_range = r - first_row[k];
     const int64_t take = std::min(counts[k] - in_range, r1 - r);
     if (take <= 0) continue;
-    std::memcpy(dst + r * row_bytes, src + (starts[k] + in_range) * row_bytes,
-                static_cast<size_t>(take * row_bytes));
+    copy_bytes(dst + r * row_bytes, src + (starts[k] + in_range) * row_bytes,
+               static_cast<size_t>(take * row_bytes));
     r += take;
   }
+  // nontemporal stores are weakly ordered: drain them before the caller learns the copy is done
+  if (EVS_HOST_NT_STORES) __builtin_ia32_sfence();
 }
 
 }  // namespace

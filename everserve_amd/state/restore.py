@@ -9,8 +9,12 @@ maps it from shared memory as ``[num_slots, 2, d]``, gathers the written rows on
 :class:`Restorer` does the same table by table, in chunks, and keeps three things busy at once:
 host threads gathering chunk i+1's rows into one pinned buffer (``evs_host_gather_ranges``), the
 copy engine moving chunk i from the other pinned buffer to the device (``evs_copy_rows_async``),
-and the scatter kernel writing chunk i into the cache (``evs_scatter_rows``). Rows land byte for
-byte where ``write_rows`` puts them.
+and the scatter kernel writing chunk i-1 into the cache (``evs_scatter_rows``). The copies run on
+a stream of their own, so the copy engine goes from one chunk to the next without waiting for
+the scatter of the previous one; events order each scatter after its copy and each copy after
+the scatter that last read its device buffer. A chunk of one slot range gets its slot ids from
+``torch.arange`` on the device instead of a second copy. Rows land byte for byte where
+``write_rows`` puts them.
 """
 
 from __future__ import annotations
@@ -103,7 +107,11 @@ class Restorer:
         self._dev = [torch.empty(n * rb, dtype=torch.uint8, device=self.device) for _ in range(2)]
         self._dev_slots = [torch.empty(n, dtype=torch.long, device=self.device) for _ in range(2)]
         self._heads: dict[int, torch.Tensor] = {}
-        self._done: list[torch.cuda.Event | None] = [None, None]
+        self._copy_stream = torch.cuda.Stream(device=self.device)
+        # per buffer: its last copy to the device (the pinned buffer is free after it) and its last
+        # scatter (the device buffer is free after it)
+        self._copied: list[torch.cuda.Event | None] = [None, None]
+        self._scattered: list[torch.cuda.Event | None] = [None, None]
         self.timing: dict[str, float] = {}
 
     def _head(self, h: int) -> torch.Tensor:
@@ -149,26 +157,38 @@ class Restorer:
                 st[0] += skip
                 ct[0] -= skip
                 ct[-1] -= first_row[k1] - c1 if k1 <= len(counts) else 0
-                done = self._done[buf]
-                if done is not None:
-                    done.synchronize()  # the copy out of this pinned buffer has finished
+                if self._copied[buf] is not None:
+                    self._copied[buf].synchronize()  # the copy out of this pinned buffer is done
                 got = self._ext.host_gather_ranges(src, table.rows.nbytes // rb, rb, st, ct,
                                                    self._host[buf].data_ptr(), n_chunk,
                                                    self._threads)
                 assert got == c1 - c0
-                slots = self._host_slots[buf].numpy()
-                at = 0
-                for s, c in zip(st.tolist(), ct.tolist()):
-                    slots[at:at + c] = np.arange(s, s + c, dtype=np.int64)
-                    at += c
                 n = c1 - c0
-                self._ext.copy_rows_async(self._dev[buf].data_ptr(), self._host[buf].data_ptr(),
-                                          1, n * rb, n * rb, self.device)
-                self._dev_slots[buf][:n].copy_(self._host_slots[buf][:n], non_blocking=True)
+                one_range = len(st) == 1
+                if not one_range:
+                    slots = self._host_slots[buf].numpy()
+                    at = 0
+                    for s, c in zip(st.tolist(), ct.tolist()):
+                        slots[at:at + c] = np.arange(s, s + c, dtype=np.int64)
+                        at += c
+                with torch.cuda.stream(self._copy_stream):
+                    if self._scattered[buf] is not None:
+                        self._copy_stream.wait_event(self._scattered[buf])
+                    self._ext.copy_rows_async(self._dev[buf].data_ptr(),
+                                              self._host[buf].data_ptr(), 1, n * rb, n * rb,
+                                              self.device)
+                    if not one_range:
+                        self._dev_slots[buf][:n].copy_(self._host_slots[buf][:n],
+                                                       non_blocking=True)
+                    self._copied[buf] = self._copy_stream.record_event()
+                if one_range:
+                    torch.arange(int(st[0]), int(st[0]) + n, dtype=torch.long, device=self.device,
+                                 out=self._dev_slots[buf][:n])
+                stream.wait_event(self._copied[buf])
                 self._ext.scatter_rows(layer_ptr, self._dev_slots[buf][:n], head,
                                        self._dev[buf].data_ptr(), n, self.paged.head_dim,
                                        self.paged.block_size, self._strides, self._elem)
-                self._done[buf] = stream.record_event()
+                self._scattered[buf] = stream.record_event()
                 total += n
                 buf ^= 1
         torch.cuda.synchronize(self.device)
