@@ -162,7 +162,9 @@ class Restorer:
                 got = self._ext.host_gather_ranges(src, table.rows.nbytes // rb, rb, st, ct,
                                                    self._host[buf].data_ptr(), n_chunk,
                                                    self._threads)
-                assert got == c1 - c0
+                if got != c1 - c0:
+                    raise RuntimeError(f"table {table.table}: gathered {got} rows of chunk "
+                                       f"[{c0}, {c1})")
                 n = c1 - c0
                 one_range = len(st) == 1
                 if not one_range:

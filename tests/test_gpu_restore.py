@@ -110,3 +110,31 @@ def test_ranges_outside_a_table_and_partial_rows_are_refused(ext):
     with pytest.raises(ValueError, match="whole number"):
         r.restore([Table(0, rows[:-5], [(0, 1)])], {0: 0})
     assert not dst[0].any()
+
+
+def test_many_chunks_on_a_side_stream_twice_with_the_same_buffers(ext):
+    """Chunks inside one slot range (slot ids made on the device) and across several (slot ids
+    copied), the copies on the Restorer's stream and the scatters on the caller's side stream,
+    and a second restore that reuses the buffers and events of the first."""
+    nb, bs, h, d = 64, 4, 2, 64
+    src = caches("kv_first", d, torch.bfloat16, n_layers=2, nb=nb, bs=bs, h=h, seed=71)
+    rng = np.random.default_rng(71)
+    slots = sorted(rng.choice(nb * bs, size=150, replace=False).tolist() + list(range(40, 90)))
+    slots = sorted(set(slots))
+    tables, written = commit(src, slots, [0, 1], cap=len(slots))
+    ranges = {t: oracle.written_ranges(written[t]) for t in tables}
+    assert any(c > 40 for _, c in ranges[0])  # a range longer than a chunk
+    dst = [torch.zeros_like(t).cuda() for t in src]
+    r = Restorer(ext, dst, chunk_bytes=16 * 2 * d * 2, threads=2)  # 16 rows a chunk
+    side = torch.cuda.Stream()
+    want = oracle.gather_rows(src, slots, [0, 1], len(slots), d, bs, strides_of(src[0]), 2)
+    for _ in range(2):
+        for t in dst:
+            t.zero_()
+        torch.cuda.synchronize()
+        with torch.cuda.stream(side):
+            rows = r.restore([Table(t, tb, ranges[t]) for t, tb in tables.items()], {0: 1, 1: 0})
+        assert rows == len(slots) * len(src) * 2
+        cpu = [t.cpu() for t in dst]
+        got = oracle.gather_rows(cpu, slots, [1, 0], len(slots), d, bs, strides_of(cpu[0]), 2)
+        assert np.array_equal(got, want)
