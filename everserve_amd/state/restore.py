@@ -20,6 +20,7 @@ the scatter that last read its device buffer. A chunk of one slot range gets its
 from __future__ import annotations
 
 import os
+import threading
 import time
 from dataclasses import dataclass
 from typing import Iterable, Mapping, Sequence
@@ -61,9 +62,12 @@ def destination_order(slots, block_size: int | None = None) -> tuple[np.ndarray,
 class Table:
     """One store table of the lost rank: its rows and the slots written in it.
 
-    ``rows`` is the table's bytes, ``[num_slots, row_bytes]`` (a numpy array, typically a
-    read-only memory map of the table file); ``written`` the ``(start, count)`` slot ranges the
-    store names (proto/everserve/proto/mirror.proto:102-117).
+    ``rows`` is the table's bytes, ``[num_slots, row_bytes]`` (a numpy array: in memory, as
+    ``StoreTables`` holds them, or a read-only mapping of the table file); ``written`` the
+    ``(start, count)`` slot ranges the store names (proto/everserve/proto/mirror.proto:102-117).
+    The mapping lives as long as the Table. On the hosts measured, unmapping 128 MiB of shared
+    memory costs 0.8-3.4 ms, as much as gathering it: drop the tables after the restore with
+    :func:`release_later`, or map them ahead of a failure and keep them mapped.
     """
 
     table: int
@@ -80,8 +84,24 @@ class Table:
 
     @classmethod
     def open(cls, table: int, path: str, written: Sequence[tuple[int, int]]) -> "Table":
-        """The table file at ``path`` mapped read-only."""
+        """The table file at ``path`` mapped read-only (its pages are read when gathered)."""
         return cls(table, np.memmap(path, dtype=np.uint8, mode="r"), written)
+
+
+def release_later(tables: list) -> threading.Thread:
+    """Drop the restored ``tables`` (the list is emptied) on a daemon thread, so that unmapping
+    their files, which costs about as much as restoring them, does not hold up the rank that
+    resumes. The mappings go when the thread drops the last references to them; CPython unmaps
+    with the GIL released. Returns the thread, to join where the release must be complete."""
+    held = list(tables)
+    tables.clear()
+
+    def drop() -> None:
+        held.clear()
+
+    th = threading.Thread(target=drop, daemon=True, name="everserve-restore-release")
+    th.start()
+    return th
 
 
 class Restorer:
@@ -127,73 +147,81 @@ class Restorer:
         """
         t0 = time.perf_counter()
         stream = torch.cuda.current_stream(self.device)
-        rb, n_chunk = self._row_bytes, self._chunk_rows
+        rb = self._row_bytes
         total = 0
         buf = 0
         for table in tables:
             if table.head not in head_map or not table.written:
                 continue
-            if table.rows.nbytes % rb:
-                raise ValueError(f"table {table.table}: {table.rows.nbytes} bytes is not a whole "
+            nbytes = table.rows.nbytes
+            if nbytes % rb:
+                raise ValueError(f"table {table.table}: {nbytes} bytes is not a whole "
                                  f"number of {rb}-byte rows")
             starts = np.array([s for s, _ in table.written], dtype=np.int64)
             counts = np.array([c for _, c in table.written], dtype=np.int64)
             if (starts < 0).any() or (counts < 0).any() or \
-                    (starts + counts).max() * rb > table.rows.nbytes:
+                    (starts + counts).max() * rb > nbytes:
                 raise ValueError(f"table {table.table}: a written range lies outside the table")
-            first_row = np.concatenate([[0], np.cumsum(counts)])
-            rows = int(first_row[-1])
-            src = table.rows.ctypes.data
-            layer_ptr = self._ptrs[table.layer:table.layer + 1]
-            head = self._head(head_map[table.head])
-            for c0 in range(0, rows, n_chunk):
-                c1 = min(rows, c0 + n_chunk)
-                # the ranges, trimmed to output rows [c0, c1)
-                k0 = int(np.searchsorted(first_row, c0, side="right")) - 1
-                k1 = int(np.searchsorted(first_row, c1, side="left"))
-                st = starts[k0:k1].copy()
-                ct = counts[k0:k1].copy()
-                skip = c0 - first_row[k0]
-                st[0] += skip
-                ct[0] -= skip
-                ct[-1] -= first_row[k1] - c1 if k1 <= len(counts) else 0
-                if self._copied[buf] is not None:
-                    self._copied[buf].synchronize()  # the copy out of this pinned buffer is done
-                got = self._ext.host_gather_ranges(src, table.rows.nbytes // rb, rb, st, ct,
-                                                   self._host[buf].data_ptr(), n_chunk,
-                                                   self._threads)
-                if got != c1 - c0:
-                    raise RuntimeError(f"table {table.table}: gathered {got} rows of chunk "
-                                       f"[{c0}, {c1})")
-                n = c1 - c0
-                one_range = len(st) == 1
-                if not one_range:
-                    slots = self._host_slots[buf].numpy()
-                    at = 0
-                    for s, c in zip(st.tolist(), ct.tolist()):
-                        slots[at:at + c] = np.arange(s, s + c, dtype=np.int64)
-                        at += c
-                with torch.cuda.stream(self._copy_stream):
-                    if self._scattered[buf] is not None:
-                        self._copy_stream.wait_event(self._scattered[buf])
-                    self._ext.copy_rows_async(self._dev[buf].data_ptr(),
-                                              self._host[buf].data_ptr(), 1, n * rb, n * rb,
-                                              self.device)
-                    if not one_range:
-                        self._dev_slots[buf][:n].copy_(self._host_slots[buf][:n],
-                                                       non_blocking=True)
-                    self._copied[buf] = self._copy_stream.record_event()
-                if one_range:
-                    torch.arange(int(st[0]), int(st[0]) + n, dtype=torch.long, device=self.device,
-                                 out=self._dev_slots[buf][:n])
-                stream.wait_event(self._copied[buf])
-                self._ext.scatter_rows(layer_ptr, self._dev_slots[buf][:n], head,
-                                       self._dev[buf].data_ptr(), n, self.paged.head_dim,
-                                       self.paged.block_size, self._strides, self._elem)
-                self._scattered[buf] = stream.record_event()
-                total += n
-                buf ^= 1
+            rows, buf = self._restore_table(table, starts, counts, head_map[table.head], stream,
+                                            buf)
+            total += rows
         torch.cuda.synchronize(self.device)
         self.timing = {"copy_s": time.perf_counter() - t0, "rows": total,
                        "bytes": total * rb}
         return total
+
+    def _restore_table(self, table: Table, starts: np.ndarray, counts: np.ndarray,
+                       new_head: int, stream, buf: int) -> tuple[int, int]:
+        """Enqueue one table's chunks, the first into buffer ``buf``: gathered from its rows,
+        copied to the device, scattered at head slot ``new_head``. Returns the rows enqueued and
+        the buffer the next chunk takes."""
+        rb, n_chunk = self._row_bytes, self._chunk_rows
+        first_row = np.concatenate([[0], np.cumsum(counts)])
+        rows = int(first_row[-1])
+        layer_ptr = self._ptrs[table.layer:table.layer + 1]
+        head = self._head(new_head)
+        for c0 in range(0, rows, n_chunk):
+            c1 = min(rows, c0 + n_chunk)
+            n = c1 - c0
+            # the ranges, trimmed to output rows [c0, c1)
+            k0 = int(np.searchsorted(first_row, c0, side="right")) - 1
+            k1 = int(np.searchsorted(first_row, c1, side="left"))
+            st = starts[k0:k1].copy()
+            ct = counts[k0:k1].copy()
+            skip = c0 - first_row[k0]
+            st[0] += skip
+            ct[0] -= skip
+            ct[-1] -= first_row[k1] - c1 if k1 <= len(counts) else 0
+            if self._copied[buf] is not None:
+                self._copied[buf].synchronize()  # the copy out of this pinned buffer is done
+            got = self._ext.host_gather_ranges(table.rows.ctypes.data, table.rows.nbytes // rb,
+                                               rb, st, ct, self._host[buf].data_ptr(), n_chunk,
+                                               self._threads)
+            if got != n:
+                raise RuntimeError(f"table {table.table}: gathered {got} rows of chunk "
+                                   f"[{c0}, {c1})")
+            one_range = len(st) == 1
+            if not one_range:
+                slots = self._host_slots[buf].numpy()
+                at = 0
+                for s, c in zip(st.tolist(), ct.tolist()):
+                    slots[at:at + c] = np.arange(s, s + c, dtype=np.int64)
+                    at += c
+            with torch.cuda.stream(self._copy_stream):
+                if self._scattered[buf] is not None:
+                    self._copy_stream.wait_event(self._scattered[buf])
+                self._ext.copy_rows_async(self._dev[buf].data_ptr(), self._host[buf].data_ptr(),
+                                          1, n * rb, n * rb, self.device)
+                if not one_range:
+                    self._dev_slots[buf][:n].copy_(self._host_slots[buf][:n], non_blocking=True)
+                self._copied[buf] = self._copy_stream.record_event()
+            if one_range:
+                torch.arange(int(st[0]), int(st[0]) + n, dtype=torch.long, device=self.device,
+                             out=self._dev_slots[buf][:n])
+            stream.wait_event(self._copied[buf])
+            self._ext.scatter_rows(layer_ptr, self._dev_slots[buf][:n], head,
+                                   self._dev[buf].data_ptr(), n, self.paged.head_dim,
+                                   self.paged.block_size, self._strides, self._elem)
+            self._scattered[buf] = stream.record_event()
+            buf ^= 1
+        return rows, buf

@@ -64,3 +64,4 @@ def test_bad_ranges_are_refused(ext):
     # the whole table into exactly enough room is fine
     assert ext.host_gather_ranges(table.ctypes.data, 4, 16, np.array([0]), np.array([4]),
                                   dst.ctypes.data, 4) == 4
+

@@ -48,3 +48,21 @@ def test_empty_and_all_padding():
     for slots in ([], [-1, -1, -1, -1]):
         got, rows_of = destination_order(slots, block_size=4)
         assert got.size == 0 and rows_of.size == 0
+
+
+def test_release_later_drops_the_tables_off_the_calling_thread(tmp_path):
+    import gc
+    import threading
+    import weakref
+
+    from everserve_amd.state.restore import Table, release_later
+
+    path = tmp_path / "table.rows"
+    np.zeros(4096, dtype=np.uint8).tofile(path)
+    tables = [Table.open(7, str(path), [(0, 8)]) for _ in range(3)]
+    maps = [weakref.ref(t.rows) for t in tables]
+    th = release_later(tables)
+    assert tables == [] and isinstance(th, threading.Thread)
+    th.join()
+    gc.collect()
+    assert all(m() is None for m in maps)
