@@ -281,3 +281,51 @@ def test_special_values_round_as_the_oracle_does(ext, push):
         assert np.array_equal(bits(out), want)
     finally:
         reg.close()
+
+
+@pytest.mark.parametrize("push", [False, True])
+def test_a_push_cut_short_is_named_by_the_blocks_still_waiting(ext, push):
+    """The dead member's last call delivered block 0's words and none after them
+    (core/tests/test_slot_kernel.py:108-122): block 0 sums every member and finishes, the blocks
+    still waiting name the member in LATE until ABORT releases them, LATE is cleared after, and
+    the words that never came sum as zeros."""
+    rows, n = [0, 1], 16384
+    per_block = 256  # words of one block at 1 word per thread: 512 elements
+    reg = Region(ext, push, rows)
+    released = False
+    try:
+        order, seqs = reg.member(rows)
+        x0, x1 = member_input(0, n), member_input(1, n)
+        w = ll_words(x1, 1)[:per_block]
+        half = MAXN // 2
+        if push:
+            at = (1 * MAXW + 1) * half  # parity 1, sender 1, in reader 0's buffer
+            reg.words[0][at:at + per_block] = w
+        else:
+            reg.words[1][half:half + per_block] = w  # sender 1's own buffer, parity 1
+        reg.ctrl[0 * CTRL_WORDS + BOUND] = 1_000_000  # name after 1 ms
+        out = torch.empty(n, dtype=torch.bfloat16, device="cuda")
+        xin = x0.cuda()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        ext.slot_all_reduce(xin, out, reg.bufs, reg.ctrl_dev, order, seqs, 0, MAXN, 1, push)
+        seen = set()
+        while time.perf_counter() - t0 < 0.2:
+            seen.add(int(reg.ctrl[LATE]))
+            time.sleep(0.001)
+        reg.ctrl[ABORT] = 1
+        released = True
+        torch.cuda.synchronize()
+        assert (1 << 1) in seen and seen <= {0, 1 << 1}, seen
+        assert int(reg.ctrl[LATE]) == 0
+        got = bits(out)
+        full = oracle.member_sum([bits(x0), bits(x1)])
+        alone = oracle.member_sum([bits(x0), None])
+        e = 2 * per_block
+        assert np.array_equal(got[:e], full[:e])  # block 0 had every word
+        assert np.array_equal(got[e:], alone[e:])  # the rest never came: zeros
+    finally:
+        if not released:
+            reg.ctrl[ABORT] = 1
+            torch.cuda.synchronize()
+        reg.close()
