@@ -1137,20 +1137,29 @@ def main(argv=None):
         result["extra"]["c2_gather_blocks"] = {
             "ms": round(bms, 4), "gbs": round(c2["algo_bytes"] / bms / 1e6, 1),
             "rows_equal_gather_rows": c2["blocks_equal"]}
+    failed = []
     if not a.quick:
         for name, fn in legs:
             if wanted and name not in wanted:
                 continue
             log(f"{name} ...")
-            result["extra"][name] = fn(ext, a.steps, a.warmup)
+            # the headline is measured: a leg that fails is recorded, and the line still printed
+            try:
+                result["extra"][name] = fn(ext, a.steps, a.warmup)
+            except Exception as e:  # noqa: BLE001
+                log(f"{name} failed: {type(e).__name__}: {e}")
+                result["extra"][name] = {"error": f"{type(e).__name__}: {e}"}
+                failed.append(name)
     if not a.no_cpu:
         log("cpu baseline ...")
         result["cpu_baseline"] = cpu_baseline_c2()
         if not a.quick and not wanted:
             log("cpu baselines of the restore and the reduce ...")
             result["extra"]["cpu_baselines_more"] = cpu_baselines_more()
+    if failed:
+        result["extra"]["failed_legs"] = failed
     print(json.dumps(result), flush=True)
-    return 0
+    return 1 if failed else 0
 
 
 if __name__ == "__main__":
