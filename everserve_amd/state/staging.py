@@ -244,8 +244,10 @@ class StepStager:
         self._in_flight_lock = threading.Lock()
         self._failed: BaseException | None = None
         self.stats = {"steps": 0, "step_thread_s": 0.0, "backpressure_waits": 0,
-                      "backpressure_s": 0.0, "bytes_staged": 0, "copy_s": 0.0}
-        """``step_thread_s`` is what commits cost the step thread, ``backpressure_s`` included."""
+                      "backpressure_s": 0.0, "bytes_staged": 0, "bytes_sent": 0, "copy_s": 0.0}
+        """``step_thread_s`` is what commits cost the step thread, ``backpressure_s`` included.
+        ``bytes_staged`` counts every row copied to the host, padding included; ``bytes_sent``
+        only the rows of real slots, as the reference's record does (mirror.py:785-787)."""
         self._copy_stream = torch.cuda.Stream(device=self.device)
         self._ready = ext.event_create(True)  # the host reads what this one orders
         self._queue: queue.Queue[StagedJob | None] = queue.Queue()
@@ -493,9 +495,12 @@ class StepStager:
             job.times["ready"] = t1 = time.perf_counter()
             self.stats["copy_s"] += t1 - t0
             self.stats["bytes_staged"] += len(g.filled) * heads * n * row_bytes
+            slots = st.host_slots[:n].tolist()
+            self.stats["bytes_sent"] += (sum(1 for x in slots if x >= 0) * row_bytes
+                                         * len(g.filled) * heads)
             job.descriptor = describe(st.name, sorted(g.filled), g.heads, st.capacity,
-                                      self.paged.head_dim, self._kernel.elem,
-                                      st.host_slots[:n].tolist(), DTYPE_NAMES[self.dtype])
+                                      self.paged.head_dim, self._kernel.elem, slots,
+                                      DTYPE_NAMES[self.dtype])
             job.stage_bytes = st.host_bytes()
             self._sink(job)
             job.times["sent"] = time.perf_counter()

@@ -93,6 +93,12 @@ def test_steps_land_in_the_store_as_the_oracle_puts_them(ext):
                 t.neg_()
         st.flush()
         assert st.stats["steps"] == len(steps)
+        row_bytes = 2 * D * 2
+        assert st.stats["bytes_sent"] == sum(
+            sum(1 for x in slots if x >= 0) * len(layers) * len(HEADS) * row_bytes
+            for slots, layers in steps)
+        assert st.stats["bytes_staged"] == sum(
+            len(slots) * len(layers) * len(HEADS) * row_bytes for slots, layers in steps)
     want = expected(states, steps)
     assert sorted(store.tables) == sorted(want)
     for table in want:
