@@ -45,7 +45,7 @@ def log(msg: str) -> None:
 
 # ------------------------------------------------------------------------------ helpers
 def layout_strides(t):
-    from everserve_amd.state.kvcopy import PagedKV
+    from everserve_amd.state.paged import PagedKV
 
     return list(PagedKV.of(t).layout_strides(t))
 
@@ -551,7 +551,7 @@ def bench_restore_host(ext, steps, warmup):
     import numpy as np
     import torch
 
-    from everserve_amd.state.kvcopy import PagedKV
+    from everserve_amd.state.paged import PagedKV
     from everserve_amd.state.restore import Restorer, Table, release_later
 
     L, NB, BS, H, D = 4, 16384, 16, 8, 128

@@ -163,6 +163,8 @@ _SIGNATURES: tuple[tuple[str, object, tuple], ...] = (
     ("evs_memset_async", _I32, (_P, _I64, _P)),
     ("evs_copy_rows_async", _I32, (_P, _P, _I64, _I64, _I64, _P)),
     ("evs_host_gather_ranges", _I32, (_P, _I64, _I64, _P, _P, _I64, _P, _I64, _I64, _P)),
+    ("evs_host_gather_tables", _I32, (_P, _I64, _I64, _I64, _P, _P, _I64, _P, _I64, _I64, _P)),
+    ("evs_deliver_rows", _I32, (_P, _I64, _P, _I64, _I64, _I64, _P, _P, _I64, _I64, _P)),
     ("evs_store_commit", _I32,
      (_P, _I64, _P, _I64, _P, _P, _P, _I64, _I64, _P, _I64, ctypes.c_uint64, _I64, _P)),
     ("evs_crc32c", _I32, (_P, _I64, _P)),
@@ -453,6 +455,42 @@ class Kernels:
         )
         return rows.value
 
+    def host_gather_tables(self, src_ptrs: Sequence[int], src_rows: int, row_bytes: int, starts,
+                           counts, dst_ptr: int, dst_rows: int, max_threads: int = 16) -> int:
+        """:meth:`host_gather_ranges` over several tables with the same ranges, in one call:
+        table j's rows land at ``dst_ptr + j * dst_rows * row_bytes``. Returns the rows copied per
+        table."""
+        import numpy as np
+
+        st = np.ascontiguousarray(starts, dtype=np.int64)
+        ct = np.ascontiguousarray(counts, dtype=np.int64)
+        if st.shape != ct.shape:
+            raise RuntimeError("host_gather_tables: starts and counts differ in length")
+        srcs = (ctypes.c_void_p * max(1, len(src_ptrs)))(*[int(p) for p in src_ptrs])
+        rows = ctypes.c_int64()
+        self._check(
+            self._lib.evs_host_gather_tables(srcs, len(src_ptrs), int(src_rows), int(row_bytes),
+                                             st.ctypes.data, ct.ctypes.data, st.size,
+                                             int(dst_ptr), int(dst_rows), int(max_threads),
+                                             ctypes.byref(rows))
+        )
+        return rows.value
+
+    def deliver_rows(self, dst_ptr: int, dst_pitch: int, src_ptr: int, src_pitch: int, runs: int,
+                     run_bytes: int, bounce: Sequence[int], bounce_bytes: int, stream,
+                     max_threads: int = 16) -> None:
+        """Copy ``runs`` runs of device rows into host memory that need not be pinned (a staging
+        file), through the two pinned ``bounce`` buffers; blocks until the rows are there.
+        ``stream`` is a torch stream the copies are issued on."""
+        if len(bounce) != 2:
+            raise RuntimeError("deliver_rows: two bounce buffers")
+        self._check(
+            self._lib.evs_deliver_rows(int(dst_ptr), int(dst_pitch), int(src_ptr), int(src_pitch),
+                                       int(runs), int(run_bytes), int(bounce[0]), int(bounce[1]),
+                                       int(bounce_bytes), int(max_threads),
+                                       int(stream.cuda_stream))
+        )
+
     # -------------------------------------------------------------- the store's commit copy
     def store_commit(self, stage, stage_offsets, tables, written_step, crc, num_slots: int,
                      row_bytes: int, slots, step: int, max_threads: int = 16) -> int:
@@ -684,53 +722,55 @@ class Kernels:
 
 
 _SOURCE: str = ""
-"""How this process got its kernels, once loaded: ``prebuilt`` or ``in-tree``."""
+"""Where this process's library came from once :func:`load` has run: ``prebuilt`` (the directory
+``EVERSERVE_KERNELS_DIR`` names) or ``in-tree``."""
 
 
 @functools.lru_cache(maxsize=1)
 def load() -> Kernels:
-    """The kernels for this process: the named prebuilt, else the in-tree build.
-
-    Cached for the process, like the HIP context the library runs in.
+    """This process's :class:`Kernels`, opened once and kept (the library lives in the process's
+    one HIP runtime, as torch does).
 
     Raises:
-        KernelsUnavailable: without a GPU, or when the build cannot be loaded here.
+        KernelsUnavailable: on a host without a GPU, or for a library whose stamp is not this
+            tree's, names another GPU, or fails to open.
     """
     global _SOURCE
     import torch
 
     if not torch.cuda.is_available():
-        raise KernelsUnavailable("the Everserve MI355X kernels need a GPU")
-    named = os.environ.get(PREBUILT_ENV, "")
+        raise KernelsUnavailable("no GPU in this process: the MI355X kernels cannot run")
     path = library_path()
     try:
         lib = open_library(path)
     except OSError as e:
-        raise KernelsUnavailable(f"{path}: cannot be loaded: {e}") from e
-    _SOURCE = "prebuilt" if named else "in-tree"
-    return Kernels(lib, path)
+        raise KernelsUnavailable(f"{path} did not open: {e}") from e
+    kernels = Kernels(lib, path)
+    _SOURCE = "prebuilt" if os.environ.get(PREBUILT_ENV) else "in-tree"
+    return kernels
 
 
 def source() -> str:
-    """How this process got its kernels: ``prebuilt``, ``in-tree``, or ``""`` before loading."""
+    """``prebuilt`` or ``in-tree`` once :func:`load` has run; empty before."""
     return _SOURCE
 
 
 @functools.lru_cache(maxsize=1)
 def available() -> bool:
-    """Whether this process runs on the kernels: False without a GPU, or by choice.
+    """True when this process moves KV and reduces on the kernels.
 
-    ``EVERSERVE_KERNELS=torch`` takes the torch paths without loading anything. Any other reason
-    the kernels cannot load raises, so a rank never runs other paths than its peers' without an
-    operator having said so (core/everserve/kernels.py:202-221).
+    Three answers, and no fourth:
 
-    Raises:
-        KernelsUnavailable: a build that cannot be loaded here.
+    * ``EVERSERVE_KERNELS=torch`` was set: False, and nothing is loaded. Only an operator's
+      choice makes a rank leave the kernels, so that every rank of an engine runs the same code;
+    * the process has no GPU: False;
+    * otherwise the library is loaded, and True; a library that cannot be loaded raises
+      :class:`KernelsUnavailable` here rather than sending this rank down another path.
     """
     import torch
 
     if os.environ.get(PATHS_ENV, "") == "torch":
-        log.info("%s=torch: the torch paths serve, the kernels are not loaded", PATHS_ENV)
+        log.info("kernels not loaded: %s=torch chose the torch paths", PATHS_ENV)
         return False
     if not torch.cuda.is_available():
         return False

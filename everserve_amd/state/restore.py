@@ -6,15 +6,20 @@ maps it from shared memory as ``[num_slots, 2, d]``, gathers the written rows on
 ``PagedKV.write_rows`` into the head slot the rank assigned. Published at 2.1-2.6 GB/s
 (bench/runs/2026-10-05-shm-commit-4gpu/RESULT.md:36,45-46): the host gather bounds it.
 
-:class:`Restorer` does the same table by table, in chunks, and keeps three things busy at once:
-host threads gathering chunk i+1's rows into one pinned buffer (``evs_host_gather_ranges``), the
-copy engine moving chunk i from the other pinned buffer to the device (``evs_copy_rows_async``),
-and the scatter kernel writing chunk i-1 into the cache (``evs_scatter_rows``). The copies run on
-a stream of their own, so the copy engine goes from one chunk to the next without waiting for
-the scatter of the previous one; events order each scatter after its copy and each copy after
-the scatter that last read its device buffer. A chunk of one slot range gets its slot ids from
-``torch.arange`` on the device instead of a second copy. Rows land byte for byte where
-``write_rows`` puts them.
+:class:`Restorer` first checks every table against this rank's cache (its layers, head slots,
+row size and slot count), so a bad table refuses the restore before anything is written. It then
+groups the tables of a layer that share their written ranges (a store commit writes every held
+head of a layer at the same slots) and restores each group in chunks, keeping three things busy
+at once: host threads gathering chunk i+1's rows of all the group's tables side by side into one
+pinned buffer (``evs_host_gather_tables``), the copy engine moving chunk i from the other pinned
+buffer to the device (``evs_copy_rows_async``), and one scatter launch writing chunk i-1 into
+every head slot of the group (``evs_scatter_rows`` with the group's head slots, the layer's own
+strides). Writing all of a layer's heads in one launch covers each cache block's rows whole, in
+increasing slot order. The copies run on a stream of their own, so the copy engine goes from one
+chunk to the next without waiting for the scatter of the previous one; events order each scatter
+after its copy and each copy after the scatter that last read its device buffer. A chunk of one
+slot range gets its slot ids from ``torch.arange`` on the device instead of a second copy. Rows
+land byte for byte where ``write_rows`` puts them.
 """
 
 from __future__ import annotations
@@ -28,7 +33,7 @@ from typing import Iterable, Mapping, Sequence
 import numpy as np
 import torch
 
-from everserve_amd.state.kvcopy import PagedKV
+from everserve_amd.state.paged import PagedKV
 
 HEAD_STRIDE = 1_000
 """A table id is layer * 1000 + head slot (core/everserve/state/mirror.py:59)."""
@@ -104,29 +109,58 @@ def release_later(tables: list) -> threading.Thread:
     return th
 
 
+@dataclass
+class _Group:
+    """Tables of one layer with the same written ranges: scattered together, one launch a chunk."""
+
+    layer: int
+    starts: np.ndarray
+    counts: np.ndarray
+    tables: list[Table]
+    heads: list[int]
+    """The head slot each table is written into, in the order of ``tables``."""
+
+
 class Restorer:
-    """Writes restored tables into ``layers`` (this rank's caches, in layer order)."""
+    """Writes restored tables into ``layers`` (this rank's caches, in layer order).
+
+    ``scales`` (optional): this rank's per-layer fp32 scale array on the device, ``[L]`` or
+    ``[L, k]``, for an fp8 cache; :meth:`restore` writes the scales that travelled beside the rows
+    into it. The rows themselves move as raw bytes and are never rescaled.
+    """
 
     def __init__(self, ext, layers: Sequence[torch.Tensor], chunk_bytes: int = 64 << 20,
-                 threads: int | None = None) -> None:
+                 threads: int | None = None, scales: torch.Tensor | None = None) -> None:
         first = layers[0]
         self._ext = ext
         self.layers = list(layers)
-        self.paged = PagedKV.of(first)
         self.device = first.device
+        self._geometry = [PagedKV.of(t) for t in layers]
+        self.paged = self._geometry[0]
+        for t, g in zip(layers, self._geometry):
+            if t.dtype != first.dtype or t.device != first.device:
+                raise ValueError("every layer's cache must have one dtype and one device")
+            if g.block_size != self.paged.block_size or g.head_dim != self.paged.head_dim:
+                raise ValueError("every layer's cache must have one block size and head size")
         self._ptrs = torch.tensor([t.data_ptr() for t in layers], dtype=torch.long,
                                   device=self.device)
-        self._strides = list(self.paged.layout_strides(first))
+        self._strides = [list(g.layout_strides(t)) for t, g in zip(layers, self._geometry)]
         self._elem = first.element_size()
         self._row_bytes = 2 * self.paged.head_dim * self._elem
-        self._chunk_rows = max(1, chunk_bytes // self._row_bytes)
+        self._chunk_bytes = max(self._row_bytes, chunk_bytes // self._row_bytes * self._row_bytes)
         self._threads = threads or min(16, len(os.sched_getaffinity(0)))
-        n, rb = self._chunk_rows, self._row_bytes
-        self._host = [torch.empty(n * rb, dtype=torch.uint8, pin_memory=True) for _ in range(2)]
-        self._host_slots = [torch.empty(n, dtype=torch.long, pin_memory=True) for _ in range(2)]
-        self._dev = [torch.empty(n * rb, dtype=torch.uint8, device=self.device) for _ in range(2)]
-        self._dev_slots = [torch.empty(n, dtype=torch.long, device=self.device) for _ in range(2)]
-        self._heads: dict[int, torch.Tensor] = {}
+        self.scales = scales
+        if scales is not None and (scales.device != self.device or scales.dtype != torch.float32
+                                   or scales.shape[0] != len(layers)):
+            raise ValueError("scales: a float32 device tensor with one entry per layer")
+        nb, rows = self._chunk_bytes, self._chunk_bytes // self._row_bytes
+        self._host = [torch.empty(nb, dtype=torch.uint8, pin_memory=True) for _ in range(2)]
+        self._host_slots = [torch.empty(rows, dtype=torch.long, pin_memory=True)
+                            for _ in range(2)]
+        self._dev = [torch.empty(nb, dtype=torch.uint8, device=self.device) for _ in range(2)]
+        self._dev_slots = [torch.empty(rows, dtype=torch.long, device=self.device)
+                           for _ in range(2)]
+        self._heads: dict[tuple[int, ...], torch.Tensor] = {}
         self._copy_stream = torch.cuda.Stream(device=self.device)
         # per buffer: its last copy to the device (the pinned buffer is free after it) and its last
         # scatter (the device buffer is free after it)
@@ -134,72 +168,134 @@ class Restorer:
         self._scattered: list[torch.cuda.Event | None] = [None, None]
         self.timing: dict[str, float] = {}
 
-    def _head(self, h: int) -> torch.Tensor:
-        if h not in self._heads:
-            self._heads[h] = torch.tensor([h], dtype=torch.long, device=self.device)
-        return self._heads[h]
+    def _head_list(self, heads: Sequence[int]) -> torch.Tensor:
+        key = tuple(heads)
+        if key not in self._heads:
+            self._heads[key] = torch.tensor(key, dtype=torch.long, device=self.device)
+        return self._heads[key]
 
-    def restore(self, tables: Iterable[Table], head_map: Mapping[int, int]) -> int:
-        """Write every table whose head slot ``head_map`` names into its new head slot.
+    def plan(self, tables: Iterable[Table], head_map: Mapping[int, int]) -> list[_Group]:
+        """Check every table against this rank's cache and group them; nothing is enqueued.
 
-        Returns the rows written, over every table. Synchronises the device at the end, as the
-        reference's restore does (core/everserve/state/mirror.py:938-939).
+        A table whose head slot ``head_map`` does not name, or with nothing written, is skipped,
+        as the reference skips it (core/everserve/state/mirror.py:922-925). The rest must fit:
+
+        Raises:
+            ValueError: a table of a layer this rank does not have; a head slot outside the
+                layer's heads; a table that is not whole rows of this cache's row size; a written
+                range outside the table or past the cache's last slot; two tables written into
+                one (layer, head slot).
         """
-        t0 = time.perf_counter()
-        stream = torch.cuda.current_stream(self.device)
         rb = self._row_bytes
-        total = 0
-        buf = 0
+        groups: dict[tuple, _Group] = {}
+        taken: set[tuple[int, int]] = set()
         for table in tables:
             if table.head not in head_map or not table.written:
                 continue
-            nbytes = table.rows.nbytes
-            if nbytes % rb:
-                raise ValueError(f"table {table.table}: {nbytes} bytes is not a whole "
-                                 f"number of {rb}-byte rows")
+            name = f"table {table.table}"
+            layer = table.layer
+            if not 0 <= layer < len(self.layers):
+                raise ValueError(f"{name}: layer {layer}, but this rank has "
+                                 f"{len(self.layers)} layers")
+            geo = self._geometry[layer]
+            head = int(head_map[table.head])
+            if not 0 <= head < geo.num_heads:
+                raise ValueError(f"{name}: head slot {head} outside the layer's "
+                                 f"{geo.num_heads} heads")
+            if (layer, head) in taken:
+                raise ValueError(f"{name}: another table is already restored into layer "
+                                 f"{layer}, head slot {head}")
+            taken.add((layer, head))
+            rows = table.rows
+            if rows.nbytes % rb or (rows.ndim == 2 and rows.shape[1] * rows.itemsize != rb):
+                raise ValueError(f"{name}: not a whole number of this cache's {rb}-byte rows")
             starts = np.array([s for s, _ in table.written], dtype=np.int64)
             counts = np.array([c for _, c in table.written], dtype=np.int64)
-            if (starts < 0).any() or (counts < 0).any() or \
-                    (starts + counts).max() * rb > nbytes:
-                raise ValueError(f"table {table.table}: a written range lies outside the table")
-            rows, buf = self._restore_table(table, starts, counts, head_map[table.head], stream,
-                                            buf)
-            total += rows
+            ends = starts + counts
+            if (starts < 0).any() or (counts < 0).any() or ends.max() > rows.nbytes // rb:
+                raise ValueError(f"{name}: a written range lies outside the table")
+            if ends.max() > geo.num_slots:
+                raise ValueError(f"{name}: a written range ends at slot {int(ends.max())}, past "
+                                 f"this cache's {geo.num_slots} slots")
+            key = (layer, starts.tobytes(), counts.tobytes(), rows.nbytes)
+            g = groups.get(key)
+            if g is None:
+                g = groups[key] = _Group(layer, starts, counts, [], [])
+            g.tables.append(table)
+            g.heads.append(head)
+        return list(groups.values())
+
+    def restore(self, tables: Iterable[Table], head_map: Mapping[int, int],
+                scales: Mapping[int, Sequence[float]] | None = None) -> int:
+        """Write every table whose head slot ``head_map`` names into its new head slot, and the
+        per-layer ``scales`` (layer -> values) into this rank's scale array.
+
+        Every table is checked first (:meth:`plan`); a refused restore writes nothing. Returns the
+        rows written, over every table. Synchronises the device at the end, as the reference's
+        restore does (core/everserve/state/mirror.py:938-939).
+        """
+        t0 = time.perf_counter()
+        groups = self.plan(tables, head_map)
+        side = None
+        if scales:
+            if self.scales is None:
+                raise ValueError("scales given, but this Restorer has no scale array")
+            side = {int(k): np.asarray(v, dtype=np.float32).reshape(self.scales.shape[1:])
+                    for k, v in scales.items()}
+            if any(not 0 <= k < len(self.layers) for k in side):
+                raise ValueError("scales name a layer this rank does not have")
+        stream = torch.cuda.current_stream(self.device)
+        total = 0
+        buf = 0
+        for g in groups:
+            rows, buf = self._restore_group(g, stream, buf)
+            total += rows * len(g.tables)
+        if side:
+            with torch.inference_mode():
+                for layer, v in side.items():
+                    self.scales[layer].copy_(torch.from_numpy(v), non_blocking=False)
         torch.cuda.synchronize(self.device)
-        self.timing = {"copy_s": time.perf_counter() - t0, "rows": total,
-                       "bytes": total * rb}
+        rb = self._row_bytes
+        self.timing = {"copy_s": time.perf_counter() - t0, "rows": total, "bytes": total * rb,
+                       "launches": sum(-(-int(g.counts.sum()) // self._rows_per_chunk(g))
+                                       for g in groups)}
         return total
 
-    def _restore_table(self, table: Table, starts: np.ndarray, counts: np.ndarray,
-                       new_head: int, stream, buf: int) -> tuple[int, int]:
-        """Enqueue one table's chunks, the first into buffer ``buf``: gathered from its rows,
-        copied to the device, scattered at head slot ``new_head``. Returns the rows enqueued and
-        the buffer the next chunk takes."""
-        rb, n_chunk = self._row_bytes, self._chunk_rows
-        first_row = np.concatenate([[0], np.cumsum(counts)])
+    def _rows_per_chunk(self, g: _Group) -> int:
+        return max(1, self._chunk_bytes // (len(g.tables) * self._row_bytes))
+
+    def _restore_group(self, g: _Group, stream, buf: int) -> tuple[int, int]:
+        """Enqueue one group's chunks, the first into buffer ``buf``: every table's rows of a
+        slot range gathered on the host side by side, copied to the device, and scattered into
+        all of the group's head slots in one launch. Returns the rows enqueued per table and the
+        buffer the next chunk takes."""
+        rb, k = self._row_bytes, len(g.tables)
+        per = self._rows_per_chunk(g)
+        first_row = np.concatenate([[0], np.cumsum(g.counts)])
         rows = int(first_row[-1])
-        layer_ptr = self._ptrs[table.layer:table.layer + 1]
-        head = self._head(new_head)
-        for c0 in range(0, rows, n_chunk):
-            c1 = min(rows, c0 + n_chunk)
+        layer = g.layer
+        layer_ptr = self._ptrs[layer:layer + 1]
+        heads = self._head_list(g.heads)
+        srcs = [t.rows.ctypes.data for t in g.tables]
+        table_rows = g.tables[0].rows.nbytes // rb
+        for c0 in range(0, rows, per):
+            c1 = min(rows, c0 + per)
             n = c1 - c0
             # the ranges, trimmed to output rows [c0, c1)
             k0 = int(np.searchsorted(first_row, c0, side="right")) - 1
             k1 = int(np.searchsorted(first_row, c1, side="left"))
-            st = starts[k0:k1].copy()
-            ct = counts[k0:k1].copy()
+            st = g.starts[k0:k1].copy()
+            ct = g.counts[k0:k1].copy()
             skip = c0 - first_row[k0]
             st[0] += skip
             ct[0] -= skip
-            ct[-1] -= first_row[k1] - c1 if k1 <= len(counts) else 0
+            ct[-1] -= first_row[k1] - c1
             if self._copied[buf] is not None:
                 self._copied[buf].synchronize()  # the copy out of this pinned buffer is done
-            got = self._ext.host_gather_ranges(table.rows.ctypes.data, table.rows.nbytes // rb,
-                                               rb, st, ct, self._host[buf].data_ptr(), n_chunk,
-                                               self._threads)
+            got = self._ext.host_gather_tables(srcs, table_rows, rb, st, ct,
+                                               self._host[buf].data_ptr(), n, self._threads)
             if got != n:
-                raise RuntimeError(f"table {table.table}: gathered {got} rows of chunk "
-                                   f"[{c0}, {c1})")
+                raise RuntimeError(f"layer {layer}: gathered {got} rows of chunk [{c0}, {c1})")
             one_range = len(st) == 1
             if not one_range:
                 slots = self._host_slots[buf].numpy()
@@ -211,7 +307,7 @@ class Restorer:
                 if self._scattered[buf] is not None:
                     self._copy_stream.wait_event(self._scattered[buf])
                 self._ext.copy_rows_async(self._dev[buf].data_ptr(), self._host[buf].data_ptr(),
-                                          1, n * rb, n * rb, self.device)
+                                          1, k * n * rb, k * n * rb, self.device)
                 if not one_range:
                     self._dev_slots[buf][:n].copy_(self._host_slots[buf][:n], non_blocking=True)
                 self._copied[buf] = self._copy_stream.record_event()
@@ -219,9 +315,10 @@ class Restorer:
                 torch.arange(int(st[0]), int(st[0]) + n, dtype=torch.long, device=self.device,
                              out=self._dev_slots[buf][:n])
             stream.wait_event(self._copied[buf])
-            self._ext.scatter_rows(layer_ptr, self._dev_slots[buf][:n], head,
+            # the chunk is [k, n, 2, d]: staged rows of k head slots at capacity n
+            self._ext.scatter_rows(layer_ptr, self._dev_slots[buf][:n], heads,
                                    self._dev[buf].data_ptr(), n, self.paged.head_dim,
-                                   self.paged.block_size, self._strides, self._elem)
+                                   self.paged.block_size, self._strides[layer], self._elem)
             self._scattered[buf] = stream.record_event()
             buf ^= 1
         return rows, buf

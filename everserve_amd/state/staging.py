@@ -1,46 +1,65 @@
-"""The per-step snapshot: a step's committed rows, every layer and held head, to pinned host memory.
+"""The per-step snapshot: a step's committed rows, every layer and held head, into a staging file.
 
 The reference's step path is ``MirrorCommittedKV.save`` / ``commit`` / ``_gather_step`` /
 ``_staging`` / ``_describe`` (core/everserve/state/mirror.py:536-800) over ``_GatherKernel``
 (mirror.py:311-370). There, layers are marked as the forward runs. ``commit`` orders a side
 stream after the forward with an event and launches one ``gather_rows`` that writes the rows
-straight into a host-mapped staging file over PCIe. A sender thread waits for the side stream
-and sends the step's ``StagedStep`` descriptor to the store.
+straight into a host-mapped staging file, ``<rank_dir>/<prefix><k>.rows`` in shared memory, over
+PCIe. A sender thread waits for the side stream and sends the step's ``StagedStep`` descriptor to
+the node's store, which maps the file by the descriptor's ``stage`` name (store/src/shm.rs:39-45)
+and copies the named rows into its tables (store/src/storage.rs:864-957).
 
-:class:`StepStager` keeps that interface and the descriptor, and moves the data differently:
+:class:`StepStager` keeps that interface, the staging files and the descriptor, and moves the data
+differently:
 
 * **The gather runs on the producing stream**, right behind the forward's last write, into a
   staging buffer in HBM (``evs_gather_rows``, one launch for every layer). At decode sizes it
   is a few microseconds of HBM time.
 * **A fence-less event** (``evs_event_create(0)``) is recorded behind it. This costs the step
   thread a few microseconds and the device nothing.
-* **A copy thread** waits for that event on the host. Only then does it issue the copy of the
-  step's rows to pinned host memory (``evs_copy_rows_async``) on its own stream. That copy
-  uses the DMA engine while the next forward runs. When it has landed, the thread calls the
-  caller's ``sink`` with the step's descriptor and the host bytes.
+* **A copy thread** waits for that event on the host. Only then does it deliver the step's rows
+  into the stage's file (``evs_deliver_rows``): the copy engine moves them in batches into two
+  pinned bounce buffers in turn, on the thread's own stream, while host threads copy the previous
+  batch into the file with nontemporal stores. The file is mapped shared, so the bytes are the
+  store's to read as soon as the call returns. Then the thread calls the caller's ``sink`` with
+  the step's descriptor, whose ``stage`` names the file.
+
+Registering the file for the device would let the copy engine write it directly, but this GPU
+pool refuses ``hipHostRegister`` of existing memory, so the file is filled through pinned bounce
+buffers instead.
 
 Why no stream waits on another: on MI355X, a stream that waits on a pending event from another
 stream (``hipStreamWaitEvent``) slowed the Llama-3-8B-shaped decode step it followed by about
 260 us. That held with or without the event's system-scope fence. An already-completed event
 costs about nothing to wait on. Here no device queue ever waits on another.
 
-Staging buffers are pooled as in the reference (mirror.py:588-642). Capacities are
-``max(8, next_pow2(n))``, and at most ``depth + 1`` buffer pairs are kept. A buffer returns to
-the pool only after its sink has returned, so a gather never overwrites rows still being copied.
+Staging files are pooled as in the reference (mirror.py:588-642): capacities are
+``max(8, next_pow2(n))``, at most ``depth + 1`` files are kept and the rest are deleted. A file
+returns to the pool only after its sink has returned, so a gather never overwrites rows the store
+has not taken.
+
+fp8 caches carry per-layer scales that are not part of the rows: the rows move as raw bytes.
+Given ``scales`` (a float32 array on the device, one entry or one row per layer), the stager
+snapshots them with each step's gather and writes them into the staging file after the rows,
+where the descriptor (and so the store) does not look; the sink gets them as ``job.scales``.
 """
 
 from __future__ import annotations
 
+import mmap
+import os
 import queue
+import tempfile
 import threading
 import time
 from dataclasses import dataclass, field
+from pathlib import Path
 from typing import Callable, Mapping, Sequence
 
 import numpy as np
 import torch
 
-from everserve_amd.state.kvcopy import HeadSlot, PagedKV, layer_index
+from everserve_amd.state.paged import HeadSlot, PagedKV, layer_index
 
 HEAD_STRIDE = 1_000
 """Table id = layer * 1000 + head slot (core/everserve/state/mirror.py:59)."""
@@ -153,24 +172,62 @@ class GatherKernel:
                                     self._strides[layer], self.elem, slots_out=slots_out)
 
 
+_MADV_POPULATE_WRITE = 23  # Linux 5.14: fault every page of a range in, writable, at once
+
+
+def _map_stage_file(path: Path, nbytes: int) -> mmap.mmap:
+    """Create ``path`` (``nbytes``, the node's group may read it) and map it shared, every page
+    faulted in now rather than at the first delivery into it."""
+    fd = os.open(path, os.O_RDWR | os.O_CREAT | os.O_TRUNC, 0o660)
+    try:
+        os.fchmod(fd, 0o660)  # the store runs as another user of the node's group
+        os.ftruncate(fd, nbytes)
+        mapping = mmap.mmap(fd, nbytes, flags=mmap.MAP_SHARED)
+    finally:
+        os.close(fd)
+    try:
+        mapping.madvise(_MADV_POPULATE_WRITE)
+    except (OSError, ValueError):
+        np.frombuffer(mapping, dtype=np.uint8)[::mmap.PAGESIZE] = 0  # older kernels: touch
+    return mapping
+
+
 @dataclass
 class Stage:
-    """One pooled staging pair: ``[L, H, capacity, 2, d]`` rows in HBM and in pinned host memory."""
+    """One pooled staging buffer: ``[L, H, capacity, 2, d]`` rows in HBM, and the staging file
+    ``path`` the rows are delivered into (the rows, then the scale side array, if any)."""
 
     name: str
+    path: Path
     capacity: int
     num_heads: int
+    rows_bytes: int
+    mapping: mmap.mmap
     device_rows: torch.Tensor
-    host_rows: torch.Tensor
     device_slots: torch.Tensor
     host_slots: torch.Tensor
     device_blocks: torch.Tensor
     host_blocks: torch.Tensor
     """Block ids of a block round, staged through pinned memory so their upload never waits."""
+    device_scales: torch.Tensor | None = None
+    host_scales: torch.Tensor | None = None
 
-    def host_bytes(self) -> np.ndarray:
-        """The pinned rows as bytes (a view, no copy)."""
-        return self.host_rows.numpy()
+    @property
+    def file_addr(self) -> int:
+        """The address of the file's mapping in this process."""
+        return np.frombuffer(self.mapping, dtype=np.uint8).ctypes.data
+
+    def file_bytes(self) -> np.ndarray:
+        """The file's rows region as bytes (a view of the mapping, no copy)."""
+        return np.frombuffer(self.mapping, dtype=np.uint8, count=self.rows_bytes)
+
+    def release(self) -> None:
+        """Unmap and delete the file (the store maps it by name, so it goes only here)."""
+        try:
+            self.mapping.close()
+        except BufferError:  # a view of it is still held: the mapping goes with the last view
+            pass
+        self.path.unlink(missing_ok=True)
 
 
 @dataclass
@@ -195,6 +252,11 @@ class StagedJob:
     """The fence-less event behind the step's gather (0 for a step with no rows)."""
     descriptor: dict | None = None
     stage_bytes: np.ndarray | None = None
+    """The staging file's rows region, valid only while the sink runs."""
+    stage_path: Path | None = None
+    scales: np.ndarray | None = None
+    """The per-layer scales as they stood at the step's gather (a copy), when the stager has
+    them."""
     done: threading.Event = field(default_factory=threading.Event)
     error: BaseException | None = None
     times: dict = field(default_factory=dict)
@@ -205,17 +267,27 @@ class StepStager:
 
     ``kv_caches`` maps layer names to the rank's cache tensors; they are ordered by the layer
     index in their names, as the reference's ``register`` orders them (mirror.py:517-520).
-    ``heads`` are the held head slots. ``sink(job)`` runs on the copy thread with
-    ``job.descriptor`` and ``job.stage_bytes`` valid. When it returns, the staging pair goes
-    back to the pool. ``depth`` bounds the steps in flight: a commit with ``depth`` steps
-    outstanding waits for the oldest, as the reference's does (mirror.py:664-669).
+    ``heads`` are the held head slots. Staging files are ``<rank_dir>/<stage_prefix><k>.rows``,
+    the names the store's open reply gives (mirror.py:461-462,603-604); without ``rank_dir`` the
+    stager makes a directory of its own in shared memory and removes it at :meth:`close`.
+    ``sink(job)`` runs on the copy thread with ``job.descriptor``, ``job.stage_path`` and
+    ``job.stage_bytes`` (the file's rows) valid. When it returns, the file goes back to the pool.
+    ``depth`` bounds the steps in flight: a commit with ``depth`` steps outstanding waits for the
+    oldest, as the reference's does (mirror.py:664-669). ``scales`` is an optional float32 device
+    array with one entry (or row) per layer, snapshotted with every step. ``bounce_bytes`` is the
+    size of each of the two pinned buffers the rows pass through, ``copy_threads`` the host
+    threads that copy them into the file.
     """
 
     def __init__(self, ext, kv_caches: Mapping[str, torch.Tensor], heads: Sequence[HeadSlot],
                  sink: Callable[[StagedJob], None], depth: int = 2,
-                 stage_prefix: str = "stage") -> None:
+                 stage_prefix: str = "stage", rank_dir: str | os.PathLike | None = None,
+                 scales: torch.Tensor | None = None, bounce_bytes: int = 32 << 20,
+                 copy_threads: int = 8) -> None:
         if depth < 1:
             raise ValueError(f"depth must be at least 1, got {depth}")
+        if bounce_bytes < 64 or bounce_bytes % 64:
+            raise ValueError(f"bounce_bytes is a positive multiple of 64, got {bounce_bytes}")
         ordered = sorted((layer_index(n), n, t) for n, t in kv_caches.items())
         self.layers = [(n, t) for _, n, t in ordered]
         self._layer_of = {n: i for i, (n, _) in enumerate(self.layers)}
@@ -231,9 +303,25 @@ class StepStager:
         self._ext = ext
         self._kernel = GatherKernel(ext, [t for _, t in self.layers], self.paged)
         self._heads_dev = torch.tensor(self.heads, dtype=torch.long, device=self.device)
+        if scales is not None and (not scales.is_cuda or scales.device != self.device
+                                   or scales.dtype != torch.float32
+                                   or scales.shape[0] != len(self.layers)):
+            raise ValueError("scales: a float32 tensor on the caches' device, one entry per layer")
+        self._scales = scales
         self._sink = sink
         self._depth = depth
         self._prefix = stage_prefix
+        self._own_dir = rank_dir is None
+        if rank_dir is None:
+            shm = "/dev/shm" if os.path.isdir("/dev/shm") else None
+            rank_dir = tempfile.mkdtemp(prefix="everserve-stage-", dir=shm)
+        self.rank_dir = Path(rank_dir)
+        if not self.rank_dir.is_dir():
+            raise ValueError(f"rank_dir {self.rank_dir} is not a directory")
+        self._bounce_bytes = int(bounce_bytes)
+        self._bounce = [torch.empty(self._bounce_bytes, dtype=torch.uint8, pin_memory=True)
+                        for _ in range(2)]
+        self._copy_threads = max(1, int(copy_threads))
         self._stage_seq = 0
         self._pool: list[Stage] = []
         self._pool_lock = threading.Lock()
@@ -295,6 +383,7 @@ class StepStager:
             self._kernel.gather(g.stage.device_slots[:g.n], self._heads_dev,
                                 g.stage.device_rows.data_ptr(), g.stage.capacity,
                                 sorted(g.filled))
+            self._snapshot_scales(g.stage)
             job.gathered = self._event()
             self._ext.event_record(job.gathered, cur)
         self._enqueue(job, t0)
@@ -346,6 +435,7 @@ class StepStager:
             self._kernel.gather_blocks(g.stage.device_blocks[:len(ids)], self._heads_dev,
                                        g.stage.device_rows.data_ptr(), g.stage.capacity,
                                        g.stage.device_slots[:n])
+            self._snapshot_scales(g.stage)
             job.gathered = self._event()
             self._ext.event_record(job.gathered, torch.cuda.current_stream(self.device))
         self._enqueue(job, t0)
@@ -359,10 +449,8 @@ class StepStager:
 
         ids = blocks_to_stage(block_tables, num_computed, window.staged, self.paged.block_size)
         n = self.commit_blocks(epoch, step, ids, num_computed)
-        window.rounds += 1
-        window.blocks_copied += len(ids)
-        window.bytes_copied += n * len(self.layers) * len(self.heads) * 2 * \
-            self.paged.head_dim * self._kernel.elem
+        window.record(len(ids), n * len(self.layers) * len(self.heads) * 2
+                      * self.paged.head_dim * self._kernel.elem)
         return ids
 
     def fence(self, step: int) -> None:
@@ -390,7 +478,16 @@ class StepStager:
             self._queue.put(None)
             self._thread.join()
         with self._pool_lock:
-            self._pool.clear()
+            pool, self._pool = self._pool, []
+        for st in pool:
+            st.release()
+        if self._own_dir:
+            for left in self.rank_dir.glob(f"{self._prefix}*.rows"):
+                left.unlink(missing_ok=True)
+            try:
+                self.rank_dir.rmdir()
+            except OSError:
+                pass
         with self._events_lock:
             events, self._events = self._events, []
         for e in events + [self._ready]:
@@ -407,34 +504,53 @@ class StepStager:
         if self._failed is not None:
             raise StagingError(f"the copy thread failed: {self._failed}") from self._failed
 
-    # ---------------------------------------------------------------- staging pairs
+    # ---------------------------------------------------------------- staging files
+    def _snapshot_scales(self, stage: Stage) -> None:
+        """The scales as they stand now, behind the gather on the producing stream."""
+        if self._scales is not None:
+            with torch.inference_mode():
+                stage.device_scales.copy_(self._scales.reshape(-1), non_blocking=True)
+
     def _staging(self, n: int) -> Stage:
-        """A staging pair with capacity ``max(8, next_pow2(n))``, from the pool when one fits."""
+        """A staging file with capacity ``max(8, next_pow2(n))``, from the pool when one fits."""
         capacity = capacity_for(n)
         with self._pool_lock:
             for i, st in enumerate(self._pool):
                 if st.capacity == capacity and st.num_heads == len(self.heads):
                     return self._pool.pop(i)
         self._stage_seq += 1
+        name = f"{self._prefix}{self._stage_seq}.rows"
         shape = (len(self.layers), len(self.heads), capacity, 2, self.paged.head_dim)
-        nbytes = int(np.prod(shape)) * self._kernel.elem
+        rows_bytes = int(np.prod(shape)) * self._kernel.elem
+        n_scales = 0 if self._scales is None else self._scales.numel()
+        path = self.rank_dir / name
+        mapping = _map_stage_file(path, rows_bytes + 4 * n_scales)
         return Stage(
-            name=f"{self._prefix}{self._stage_seq}.rows",
+            name=name,
+            path=path,
             capacity=capacity,
             num_heads=len(self.heads),
-            device_rows=torch.empty(nbytes, dtype=torch.uint8, device=self.device),
-            host_rows=torch.empty(nbytes, dtype=torch.uint8, pin_memory=True),
+            rows_bytes=rows_bytes,
+            mapping=mapping,
+            device_rows=torch.empty(rows_bytes, dtype=torch.uint8, device=self.device),
             device_slots=torch.empty(capacity, dtype=torch.long, device=self.device),
             host_slots=torch.empty(capacity, dtype=torch.long, pin_memory=True),
             device_blocks=torch.empty(capacity, dtype=torch.int32, device=self.device),
             host_blocks=torch.empty(capacity, dtype=torch.int32, pin_memory=True),
+            device_scales=(None if not n_scales else
+                           torch.empty(n_scales, dtype=torch.float32, device=self.device)),
+            host_scales=(None if not n_scales else
+                         torch.empty(n_scales, dtype=torch.float32, pin_memory=True)),
         )
 
     def _release(self, stage: Stage) -> None:
-        """Return a pair to the pool, keeping at most ``depth + 1`` (mirror.py:636-642)."""
+        """Return a file to the pool, keeping at most ``depth + 1``; delete the others
+        (mirror.py:636-642)."""
         with self._pool_lock:
             if len(self._pool) <= self._depth:
                 self._pool.append(stage)
+                return
+        stage.release()
 
     def _event(self) -> int:
         with self._events_lock:
@@ -475,23 +591,29 @@ class StepStager:
             st, n = g.stage, g.n
             row_bytes = 2 * self.paged.head_dim * self._kernel.elem
             heads = len(g.heads)
-            with torch.cuda.stream(self._copy_stream):
-                if len(g.filled) == len(self.layers):
-                    self._ext.copy_rows_async(st.host_rows.data_ptr(), st.device_rows.data_ptr(),
-                                              len(self.layers) * heads, n * row_bytes,
-                                              st.capacity * row_bytes, self.device)
-                else:
-                    layer_bytes = heads * st.capacity * row_bytes
-                    for layer in sorted(g.filled):
-                        at = layer * layer_bytes
-                        self._ext.copy_rows_async(st.host_rows.data_ptr() + at,
-                                                  st.device_rows.data_ptr() + at, heads,
-                                                  n * row_bytes, st.capacity * row_bytes,
-                                                  self.device)
+            pitch = st.capacity * row_bytes
+            cs = self._copy_stream
+            bounce = [b.data_ptr() for b in self._bounce]
+            with torch.cuda.stream(cs):
+                # the small copies first: the delivery below waits for everything before it
                 self._ext.copy_rows_async(st.host_slots.data_ptr(), st.device_slots.data_ptr(),
                                           1, n * 8, n * 8, self.device)
-                self._ext.event_record(self._ready, self._copy_stream)
-            self._ext.event_synchronize(self._ready)
+                if st.device_scales is not None:
+                    nb = st.device_scales.numel() * 4
+                    self._ext.copy_rows_async(st.host_scales.data_ptr(),
+                                              st.device_scales.data_ptr(), 1, nb, nb, self.device)
+            runs = ([(0, len(self.layers) * heads)] if len(g.filled) == len(self.layers) else
+                    [(layer * heads * pitch, heads) for layer in sorted(g.filled)])
+            file_addr = st.file_addr
+            for at, count in runs:
+                self._ext.deliver_rows(file_addr + at, pitch, st.device_rows.data_ptr() + at,
+                                       pitch, count, n * row_bytes, bounce, self._bounce_bytes,
+                                       cs, self._copy_threads)
+            if st.host_scales is not None:
+                scales = st.host_scales.numpy()
+                np.frombuffer(st.mapping, dtype=np.float32, count=scales.size,
+                              offset=st.rows_bytes)[:] = scales
+                job.scales = scales.reshape(self._scales.shape).copy()
             job.times["ready"] = t1 = time.perf_counter()
             self.stats["copy_s"] += t1 - t0
             self.stats["bytes_staged"] += len(g.filled) * heads * n * row_bytes
@@ -501,7 +623,8 @@ class StepStager:
             job.descriptor = describe(st.name, sorted(g.filled), g.heads, st.capacity,
                                       self.paged.head_dim, self._kernel.elem, slots,
                                       DTYPE_NAMES[self.dtype])
-            job.stage_bytes = st.host_bytes()
+            job.stage_path = st.path
+            job.stage_bytes = st.file_bytes()
             self._sink(job)
             job.times["sent"] = time.perf_counter()
         finally:

@@ -12,6 +12,9 @@ process or links this library:
 * :meth:`StoreTables.written_ranges` and :meth:`StoreTables.restore_tables` are what a restore
   reads back: ``Layer::written_ranges`` (:430-451), as :class:`everserve_amd.state.restore.Table`
   objects.
+* An fp8 cache's per-layer scales are not in the rows. When a staged step carries them
+  (``job.scales``), the tables keep the latest beside the rows (:meth:`StoreTables.restore_scales`),
+  for the restore to write into the new cache's scale array.
 
 Tables are created on first use: ``num_slots * row_bytes`` bytes, zeroed, with every page touched
 at creation so that the first commit into them pays no page faults (``Layer::create``,
@@ -93,6 +96,8 @@ class StoreTables:
         self.threads = threads or min(16, len(os.sched_getaffinity(0)))
         self.tables: dict[int, StoreTable] = {}
         self.step = 0
+        self.scales: np.ndarray | None = None
+        """The per-layer scales of the latest step that carried them."""
 
     def _create(self, table: int, row_bytes: int) -> StoreTable:
         nbytes = self.num_slots * row_bytes
@@ -160,7 +165,15 @@ class StoreTables:
             if isinstance(t.rows, np.memmap):
                 t.rows.flush()
 
+    def restore_scales(self) -> dict[int, np.ndarray]:
+        """Layer -> its scales as last committed; empty when no step carried any."""
+        if self.scales is None:
+            return {}
+        return {layer: v.copy() for layer, v in enumerate(self.scales)}
+
     def sink(self, job) -> None:
         """A :class:`everserve_amd.state.staging.StepStager` sink: commit each staged step."""
         if job.descriptor is not None:
             self.commit(job.stage_bytes, job.descriptor, job.step)
+        if getattr(job, "scales", None) is not None:
+            self.scales = np.array(job.scales, dtype=np.float32, copy=True)

@@ -218,6 +218,31 @@ int evs_host_gather_ranges(const void* src, int64_t src_rows, int64_t row_bytes,
                            const int64_t* starts, const int64_t* counts, int64_t nranges,
                            void* dst, int64_t dst_rows, int64_t max_threads, int64_t* rows_out);
 
+/* evs_host_gather_ranges over several tables with the same written ranges (the head tables of one
+ * layer: a store commit writes every held head of a layer at the same slots): table j's rows land
+ * at dst + j * dst_rows * row_bytes, so dst holds num_tables * dst_rows rows. One call, one set of
+ * host threads for all of them. Everything is checked before anything is copied. Replaces the
+ * per-table torch.index_select of the restore (core/everserve/state/mirror.py:926-932) for a
+ * restore that scatters a layer's heads in one launch. */
+int evs_host_gather_tables(const void* const* srcs, int64_t num_tables, int64_t src_rows,
+                           int64_t row_bytes, const int64_t* starts, const int64_t* counts,
+                           int64_t nranges, void* dst, int64_t dst_rows, int64_t max_threads,
+                           int64_t* rows_out);
+
+/* Deliver `runs` runs of `run_bytes` bytes from device memory (run g at src + g * src_pitch) into
+ * host memory that need not be pinned (run g at dst + g * dst_pitch), such as a staging file in
+ * shared memory that the node's store maps by name. The copy engine moves batches of rows on
+ * `stream` into two pinned bounce buffers of `bounce_bytes` each (a positive multiple of 64) in
+ * turn, while up to max_threads host threads copy the previous batch into dst with nontemporal
+ * stores. Blocks the calling thread until every byte is in dst; run it off the step thread. The
+ * device rows must be complete before the call (the caller waits for the gather's event).
+ * Stands in for the reference's zero-copy writes through a cudaHostRegister'd staging file
+ * (core/everserve/state/mirror.py:349-356,588-634) where registering existing memory is not
+ * allowed. */
+int evs_deliver_rows(void* dst, int64_t dst_pitch, const void* src, int64_t src_pitch,
+                     int64_t runs, int64_t run_bytes, void* bounce0, void* bounce1,
+                     int64_t bounce_bytes, int64_t max_threads, void* stream);
+
 /* The node store's commit copy (store/src/storage.rs:864-957; copy loop :916-943): the rows of
  * one staged step into `ntables` store tables, on the host.
  *   stage              the staged bytes (stage_bytes long); table k's rows start at

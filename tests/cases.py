@@ -174,3 +174,21 @@ def special_members() -> dict[int, np.ndarray]:
 def bf16_tensor(raw: np.ndarray) -> torch.Tensor:
     """A CPU bf16 tensor holding the raw bits ``raw`` (uint16)."""
     return torch.from_numpy(np.ascontiguousarray(raw).view(np.int16)).view(torch.bfloat16)
+
+
+def fp8_scaled_layers(n_layers: int, shape, seed: int, device: str = "cuda"):
+    """C3's fp8-e4m3 cache: layer l holds fp8(N(0, 1) / s_l) with per-layer scales s_l ~ U(0.01,
+    0.1) (numpy rng ``seed``), saturated to e4m3's +-448 as a cast from a wider type saturates.
+    Layer 0's first 256 bytes are then overwritten with every byte code 0..255, so the NaN codes
+    (0x7F, 0xFF), the saturation codes and the subnormals are all among the bytes moved.
+
+    Returns (layers, scales) with scales a float32 numpy array [n_layers]."""
+    scales = np.random.default_rng(seed).uniform(0.01, 0.1, n_layers).astype(np.float32)
+    g = torch.Generator(device=device).manual_seed(seed)
+    out = []
+    for s in scales.tolist():
+        x = torch.randn(shape, generator=g, device=device, dtype=torch.float32)
+        out.append((x / s).clamp_(-448, 448).to(torch.float8_e4m3fn))
+    out[0].view(torch.uint8).view(-1)[:256] = torch.arange(256, dtype=torch.uint8,
+                                                           device=device)
+    return out, scales

@@ -4,8 +4,9 @@ The reference's scenario (core/tests/test_staging.py:1-116) is a cache written t
 rounds copy the blocks that changed. Here the cache is on the GPU, every layer and head slot, and
 each round goes through the product path:
 1. ``StepStager.stage_round`` plans the round and gathers the blocks with the slot tags.
-2. The rows are copied to pinned host memory.
-3. The oracle's store commit copies them into tables (store/src/storage.rs:864-957).
+2. The rows are delivered into the round's staging file in the rank directory.
+3. The oracle's store commit maps that file by its name and copies the rows into tables
+   (store/src/storage.rs:864-957).
 
 After the last round the product ``Restorer`` writes the tables' written ranges into a fresh cache
 (core/everserve/state/mirror.py:916-937). The fresh cache must equal the doomed one on every block
@@ -81,7 +82,9 @@ def test_rounds_then_restore_rebuild_every_block_in_use(ext):
         if job.descriptor is None:
             return
         tags.append(list(job.descriptor["slots"]))
-        oracle.store_commit(job.stage_bytes, job.descriptor, tables, NB * BS, written, job.step)
+        # the store maps the staging file the descriptor names, in the stager's rank directory
+        staged = np.memmap(st.rank_dir / job.descriptor["stage"], dtype=np.uint8, mode="r")
+        oracle.store_commit(np.asarray(staged), job.descriptor, tables, NB * BS, written, job.step)
 
     window = notice.StagingWindow(rank=1, deadline=0.0)
     shadow = {}

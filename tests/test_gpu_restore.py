@@ -138,3 +138,71 @@ def test_many_chunks_on_a_side_stream_twice_with_the_same_buffers(ext):
         cpu = [t.cpu() for t in dst]
         got = oracle.gather_rows(cpu, slots, [1, 0], len(slots), d, bs, strides_of(cpu[0]), 2)
         assert np.array_equal(got, want)
+
+
+def test_tables_that_do_not_fit_this_ranks_cache_are_refused_before_anything_is_written(ext):
+    """A table of a layer this rank lacks, a head slot past the layer's heads, a written range
+    past the cache's slots (a table of a larger cache), rows of another size, or two tables into
+    one head slot: each refuses the whole restore, and nothing of the good tables is written."""
+    src = caches("kv_first", 8, torch.bfloat16, n_layers=2, nb=8, bs=4, h=2, seed=62)
+    tables, written = commit(src, [0, 1, 5, 9], [0, 1], cap=8)
+    good = [Table(t, rows, oracle.written_ranges(written[t])) for t, rows in tables.items()]
+    dst = [torch.zeros_like(t).cuda() for t in src]
+    r = Restorer(ext, dst)
+    big = np.zeros(64 * 32, dtype=np.uint8)  # a table of 64 slots; this cache has 32
+    cases = [
+        (good + [Table(2000, tables[0], [(0, 2)])], {0: 0, 1: 1}, "layer 2"),
+        (good, {0: 0, 1: 2}, "head slot 2 outside"),
+        (good[:1] + [Table(1, big, [(30, 3)])], {0: 0, 1: 1}, "past this cache"),
+        (good[:1] + [Table(1, tables[0][:-8], [(0, 1)])], {0: 0, 1: 1}, "whole number"),
+        (good[:1] + [Table(1, tables[0].reshape(-1, 16), [(0, 1)])], {0: 0, 1: 1},
+         "whole number"),
+        (good + [Table(1, tables[0], [(0, 1)])], {0: 1, 1: 1}, "already restored"),
+    ]
+    for extra, moves, match in cases:
+        with pytest.raises(ValueError, match=match):
+            r.restore(extra, moves)
+        torch.cuda.synchronize()
+        assert not any(t.any() for t in dst), match
+
+
+def test_each_layer_keeps_its_own_strides(ext):
+    """Layer 1 is a view with other strides than layer 0 (the same shape, stored in another
+    dimension order): the restore addresses each layer with its own five strides."""
+    nb, bs, h, d = 16, 4, 2, 8
+    src = caches("kv_first", d, torch.bfloat16, n_layers=2, nb=nb, bs=bs, h=h, seed=63)
+    slots = [3, 4, 5, 17, 40, 63]
+    tables, written = commit(src, slots, [0, 1], cap=8)
+    dst0 = torch.zeros_like(src[0]).cuda()
+    order = [4, 3, 2, 1, 0]
+    dst1 = torch.zeros_like(src[1]).cuda().permute(order).contiguous().permute(order)
+    assert dst1.stride() != dst0.stride()
+    Restorer(ext, [dst0, dst1]).restore(
+        [Table(t, rows, oracle.written_ranges(written[t])) for t, rows in tables.items()],
+        {0: 1, 1: 0})
+    for li, dst in enumerate((dst0, dst1)):
+        cpu = dst.cpu()
+        assert np.array_equal(
+            oracle.gather_rows([cpu], slots, [1, 0], 8, d, bs, strides_of(cpu), 2),
+            oracle.gather_rows([src[li]], slots, [0, 1], 8, d, bs, strides_of(src[li]), 2)), li
+
+
+def test_a_layers_heads_are_scattered_in_one_launch_per_chunk(ext):
+    """Tables of one layer with the same written ranges form one group: the chunks carry all the
+    group's heads, so the launch count is the chunk count of one table, not of each."""
+    nb, bs, h, d = 32, 4, 4, 8
+    src = caches("blocks_first", d, torch.bfloat16, n_layers=3, nb=nb, bs=bs, h=h, seed=64)
+    slots = list(range(0, 100))
+    tables, written = commit(src, slots, [0, 1, 2, 3], cap=128)
+    dst = [torch.zeros_like(t).cuda() for t in src]
+    per_chunk_rows = 10
+    r = Restorer(ext, dst, chunk_bytes=4 * per_chunk_rows * 2 * d * 2)
+    moves = {0: 3, 1: 2, 2: 1, 3: 0}
+    rows = r.restore([Table(t, tb, oracle.written_ranges(written[t])) for t, tb in tables.items()],
+                     moves)
+    assert rows == 100 * 3 * 4
+    assert r.timing["launches"] == 3 * 10
+    cpu = [t.cpu() for t in dst]
+    assert np.array_equal(
+        oracle.gather_rows(cpu, slots, [3, 2, 1, 0], 128, d, bs, strides_of(cpu[0]), 2),
+        oracle.gather_rows(src, slots, [0, 1, 2, 3], 128, d, bs, strides_of(src[0]), 2))

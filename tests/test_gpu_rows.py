@@ -13,7 +13,8 @@ import torch
 
 import oracle
 from everserve_amd.state.restore import destination_order
-from tests.cases import (CAPACITY, DTYPES, HEADS, LAYOUTS, SLOTS, bits, caches, strides_of)
+from tests.cases import (CAPACITY, DTYPES, HEADS, LAYOUTS, SLOTS, bits, caches,
+                         fp8_scaled_layers, strides_of)
 
 pytestmark = pytest.mark.gpu
 
@@ -208,9 +209,10 @@ def test_c2_full_size_round_trip(ext):
 @pytest.mark.parametrize("layout", ["blocks_first", "combined"])
 def test_c2_shape_round_trip_in_the_other_layouts(ext, layout):
     """The C2 per-layer shape in the other two paged layouts, four layers (512 MiB each): the
-    gathered rows equal the layout's torch indexing (PagedKV.rows_of_heads, on the device), and
-    scattered into zeroed caches they restore exactly the gathered blocks, nothing else."""
-    from everserve_amd.state.kvcopy import PagedKV
+    gathered rows equal the layout's torch indexing (the reference's rows_of_heads, restated in
+    oracle.cpu_path and run on the device), and scattered into zeroed caches they restore exactly
+    the gathered blocks, nothing else."""
+    from oracle import cpu_path
 
     L, NB, BS, H, D = 4, 8192, 16, 8, 128
     shape = {"blocks_first": (NB, 2, BS, H, D), "combined": (NB, H, BS, 2 * D)}[layout]
@@ -227,23 +229,27 @@ def test_c2_shape_round_trip_in_the_other_layouts(ext, layout):
     fresh = [torch.zeros_like(t) for t in layers]
     ext.scatter_rows(ptrs(fresh), s, heads, out.data_ptr(), n, D, BS, strides, 2)
     torch.cuda.synchronize()
-    paged = PagedKV.of(layers[0])
     b = torch.from_numpy(blocks).cuda()
     keep = torch.ones(NB, dtype=torch.bool, device="cuda")
     keep[b] = False
     for li, (orig, back) in enumerate(zip(layers, fresh)):
-        want = paged.rows_of_heads(orig, s, heads)  # [H, n, 2, D]
+        want = cpu_path.rows_of_heads(orig, s, heads)  # [H, n, 2, D]
         assert torch.equal(out[li].view(torch.int16), want.contiguous().view(torch.int16)), li
         assert torch.equal(orig[b].view(torch.int16), back[b].view(torch.int16)), li
         assert not back[keep].view(torch.int16).any(), li
 
 
 def test_c3_fp8_share_gather_and_copy_to_pinned_memory(ext):
-    """C3: 80 layers of a one-head fp8 e4m3 cache, 2048 blocks gathered and copied to pinned host
-    memory; the bytes equal the oracle's on a layer subset and the device staging on all."""
+    """C3: 80 layers of a one-head fp8 e4m3 cache holding fp8(N(0,1) / s_l) with per-layer scales
+    s_l ~ U(0.01, 0.1), and every byte code in layer 0's first block; 2048 blocks gathered and
+    copied to pinned host memory. The bytes equal the oracle's on a layer subset and the device
+    staging on all."""
     L, NB, BS, H, D = 80, 8192, 16, 1, 128
-    layers = gpu_caches(L, (2, NB, BS, H, D), torch.float8_e4m3fn, seed=3)
-    _, slots = block_table(NB, 2048, BS, seed=3)
+    layers, _ = fp8_scaled_layers(L, (2, NB, BS, H, D), seed=3)
+    blocks, _ = block_table(NB, 2048, BS, seed=3)
+    if 0 not in blocks:
+        blocks[-1] = 0  # the block holding every byte code, NaN and saturation codes among them
+    slots = oracle.expand_blocks(blocks, BS)
     n = len(slots)
     staging = torch.empty((L, H, n, 2, D), dtype=torch.uint8, device="cuda")
     host = torch.zeros((L, H, n, 2, D), dtype=torch.uint8, pin_memory=True)

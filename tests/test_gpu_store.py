@@ -1,6 +1,7 @@
 """The whole per-worker path on the GPU, product code end to end, the oracle only as the checker.
 
-1. A rank's steps are staged by StepStager: the gather kernel, then D2H into pinned memory.
+1. A rank's steps are staged by StepStager: the gather kernel, then the delivery of the rows
+   into a staging file in shared memory.
 2. They are committed by StoreTables, the store's commit copy with per-row CRC32C, on host
    threads.
 3. A spare's fresh cache is rebuilt from the store's written ranges by the Restorer: host gather,

@@ -52,6 +52,20 @@ def test_the_window_counts_down_to_the_deadline():
     assert w.seconds_left(40.0) == 60.0
     assert w.seconds_left(101.0) == -1.0
     assert (w.rounds, w.blocks_copied, w.bytes_copied, w.staged) == (0, 0, 0, {})
+    w.record(5, 1000)
+    w.record(2, 24)
+    assert (w.rounds, w.blocks_copied, w.bytes_copied) == (2, 7, 1024)
+
+
+def test_a_table_that_changed_under_a_staged_request_restarts_at_the_first_changed_block():
+    staged = {}
+    assert notice.blocks_to_stage({"a": [4, 5, 6]}, {"a": 40}, staged, 16) == [4, 5, 6]
+    # recomputed into new blocks from the second one, one token more
+    assert notice.blocks_to_stage({"a": [4, 9, 8]}, {"a": 41}, staged, 16) == [8, 9]
+    assert staged["a"].tokens == 41 and staged["a"].blocks == (4, 9, 8)
+    # nothing new: nothing staged; a finished request is forgotten
+    assert notice.blocks_to_stage({"a": [4, 9, 8]}, {"a": 41}, staged, 16) == []
+    assert notice.blocks_to_stage({}, {}, staged, 16) == [] and staged == {}
 
 
 def test_block_size_must_be_positive():
