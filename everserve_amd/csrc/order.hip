@@ -6,6 +6,11 @@
 // beyond its inputs and outputs lives in a workspace the caller allocates: the row numbers
 // 0..n-1, then rocPRIM's temporary storage. rocPRIM clears its counters there with
 // hipMemsetAsync, so this call is not one to capture in a HIP graph.
+//
+// evs_order_pairs_static is the same call for callers that cannot allocate (no workspace
+// argument): its scratch is a file-scope device array of a fixed size.
+
+#include <mutex>
 
 #include <rocprim/device/device_radix_sort.hpp>
 
@@ -32,6 +37,34 @@ int sort_storage(int64_t n, int bits, size_t* bytes) {
                                     static_cast<const int64_t*>(nullptr),
                                     static_cast<int64_t*>(nullptr), static_cast<uint32_t>(n), 0u,
                                     static_cast<unsigned>(bits), hipStream_t{nullptr}));
+  return EVS_OK;
+}
+
+// The allocation-free variant's scratch: the row numbers and rocPRIM's temporary storage of a
+// call of up to EVS_ORDER_STATIC_MAX_PAIRS pairs, in a file-scope device array. Every GPU the
+// library runs on holds its own copy until the process ends. Host code never passes the array's
+// name to a kernel (in host code it is a stand-in, not a device address): the address comes from
+// hipGetSymbolAddress, once per device, with that device current.
+static __device__ __align__(256) unsigned char scratch[EVS_ORDER_STATIC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_lock;
+void* g_scratch[kMaxDevices];  // the array's address on each device, once looked up
+
+// The current device's copy of the scratch array.
+int scratch_here(void** out) {
+  int dev = -1;
+  EVS_HIP(hipGetDevice(&dev));
+  EVS_REQUIRE(dev >= 0 && dev < kMaxDevices, "evs_order_pairs_static: device %d past the %d "
+              "devices it keeps a scratch address for", dev, kMaxDevices);
+  std::lock_guard<std::mutex> hold(g_scratch_lock);
+  if (g_scratch[dev] == nullptr) {
+    void* p = nullptr;
+    EVS_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    EVS_REQUIRE(p != nullptr, "evs_order_pairs_static: no device address for the scratch");
+    g_scratch[dev] = p;
+  }
+  *out = g_scratch[dev];
   return EVS_OK;
 }
 
@@ -86,4 +119,28 @@ extern "C" int evs_order_pairs(const int64_t* slots, int64_t num_pairs, int key_
                                     static_cast<uint32_t>(num_pairs), 0u,
                                     static_cast<unsigned>(key_bits), s));
   return EVS_OK;
+}
+
+extern "C" int evs_order_pairs_static(const int64_t* slots, int64_t num_pairs, int key_bits,
+                                      int64_t* slots_out, int64_t* rows_out, void* stream) {
+  evs::clear_error();
+  EVS_REQUIRE(num_pairs >= 0 && num_pairs <= EVS_ORDER_STATIC_MAX_PAIRS,
+              "evs_order_pairs_static: %lld pairs, at most %d fit its scratch; give "
+              "evs_order_pairs a workspace for more",
+              static_cast<long long>(num_pairs), EVS_ORDER_STATIC_MAX_PAIRS);
+  int64_t need = 0;
+  int rc = evs_order_pairs_workspace(num_pairs, key_bits, &need);
+  if (rc != EVS_OK) return rc;
+  EVS_REQUIRE(need <= EVS_ORDER_STATIC_SCRATCH_BYTES,
+              "evs_order_pairs_static: %lld pairs of %d key bits need %lld bytes of scratch, "
+              "it holds %d", static_cast<long long>(num_pairs), key_bits,
+              static_cast<long long>(need), EVS_ORDER_STATIC_SCRATCH_BYTES);
+  if (num_pairs == 0) return EVS_OK;
+  void* ptr = nullptr;  // this device's copy of the scratch array
+  rc = evs::scratch_here(&ptr);
+  if (rc != EVS_OK) return rc;
+  // the row numbers are written whole by the call and rocPRIM clears its own counters, so
+  // nothing from the previous call's contents is read
+  return evs_order_pairs(slots, num_pairs, key_bits, slots_out, rows_out, ptr,
+                         EVS_ORDER_STATIC_SCRATCH_BYTES, stream);
 }

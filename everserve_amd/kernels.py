@@ -150,6 +150,7 @@ _SIGNATURES: tuple[tuple[str, object, tuple], ...] = (
      (_P, _I64, _P, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _P, _I64, _P)),
     ("evs_order_pairs_workspace", _I32, (_I64, _I32, _P)),
     ("evs_order_pairs", _I32, (_P, _I64, _I32, _P, _P, _P, _I64, _P)),
+    ("evs_order_pairs_static", _I32, (_P, _I64, _I32, _P, _P, _P)),
     ("evs_local_reduce", _I32, (_P, _P, _P, _P, _I64, ctypes.c_uint64, _I64, _P, _P, _P)),
     ("evs_slot_all_reduce", _I32,
      (_P, _P, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I32, _I64, _P)),

@@ -129,6 +129,20 @@ int evs_order_pairs_workspace(int64_t num_pairs, int key_bits, int64_t* bytes);
 int evs_order_pairs(const int64_t* slots, int64_t num_pairs, int key_bits, int64_t* slots_out,
                     int64_t* rows_out, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* evs_order_pairs without a workspace argument, for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No
+ * counterpart in the reference. Its scratch is a file-scope device array of
+ * EVS_ORDER_STATIC_SCRATCH_BYTES that every GPU the library runs on holds until the process ends;
+ * num_pairs is at most EVS_ORDER_STATIC_MAX_PAIRS (a larger call is refused with a message, and
+ * nothing is enqueued). Calls on one GPU share that GPU's array: two calls that overlap on one GPU
+ * (on different streams, or from different threads) race and give wrong results, so order them.
+ * The call allocates nothing and does not synchronise; like evs_order_pairs, rocPRIM clears its
+ * counters with hipMemsetAsync, so keep it out of captured graphs. */
+#define EVS_ORDER_STATIC_MAX_PAIRS (1 << 20)
+#define EVS_ORDER_STATIC_SCRATCH_BYTES (32 << 20)
+int evs_order_pairs_static(const int64_t* slots, int64_t num_pairs, int key_bits,
+                           int64_t* slots_out, int64_t* rows_out, void* stream);
+
 /* The reduction stage of the failure-detecting all-reduce over member buffers already in this
  * GPU's HBM (the local stage of core/csrc/slot.cu:118-224):
  *
