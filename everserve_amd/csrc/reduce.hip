@@ -10,9 +10,10 @@
 // system-scope loads (a peer's stores over xGMI, or the host's, land behind this GPU's caches),
 // in the same round of loads as the order and the buffer table, and combines the lanes with a
 // ballot. While a member is missing it polls again; every 32 polls it reads the wall clock and
-// lane 0 reads the ABORT control word. The wait ends when every flag has arrived, when ABORT is set, when
-// another workgroup of the same call gave up, or when the hard timeout passes; a member still
-// missing then contributes zeros, as the reference's aborted reads do (slot.cu:148). Past the
+// lane 0 reads the ABORT control word. The wait ends when every flag has arrived, when ABORT is
+// set, or when the hard timeout passes; a member still missing then contributes zeros, as the
+// reference's aborted reads do (slot.cu:148). Workgroups share no word that would end each
+// other's waits: each decides for itself, by the flags, ABORT and its own clock. Past the
 // BOUND control word (ns, 0 = off) the workgroup writes the rows it still waits for into LATE,
 // and the last workgroup that named clears LATE once its wait is over (slot.cu:29-40,174-214).
 // Every workgroup is resident at once and bounds its own wait by ABORT and the clock, so they

@@ -455,8 +455,10 @@ int launch_typed(RowsArgs a, int64_t L, uint32_t W, hipStream_t stream, const ch
   const int64_t grid = tiles * groups * L;
   EVS_REQUIRE(ts * per_slot < (int64_t{1} << 31), "%s: a tile of %lld words is too large", name,
               static_cast<long long>(ts * per_slot));
-  EVS_REQUIRE(grid < (int64_t{1} << 31), "%s: %lld workgroups exceed the launch limit", name,
-              static_cast<long long>(grid));
+  // HIP on AMD GPUs takes at most 2^32 - 1 work-items along x (gridDim.x * blockDim.x)
+  EVS_REQUIRE(grid * threads_of(D, I) < (int64_t{1} << 32),
+              "%s: %lld workgroups of %d threads exceed the launch limit of 2^32 - 1 work-items; "
+              "split the call by layers", name, static_cast<long long>(grid), threads_of(D, I));
   a.TS = static_cast<int>(ts);
   a.tile_words = static_cast<uint32_t>(ts * per_slot);
   a.div_w = FastDiv(W);

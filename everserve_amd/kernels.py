@@ -236,6 +236,7 @@ class Kernels:
         words = (ctypes.c_int64 * 5)()
         self._check(lib.evs_layout_constants(words, 5))
         self.MAX_ROWS, self.CTRL_WORDS, self.ABORT, self.LATE, self.BOUND = (int(w) for w in words)
+        self._workspace: dict = {}  # order_pairs' workspace, per (device, stream)
 
     def _check(self, rc: int) -> None:
         if rc != EVS_OK:
@@ -393,27 +394,41 @@ class Kernels:
                 )
             )
 
-    def order_pairs(self, slots, num_slots: int):
+    def order_pairs(self, slots, num_slots: int, out=None):
         """``(slots_sorted, rows_of)`` for :meth:`scatter_pairs`, ordered on the device.
 
         ``slots`` (int64, on the device) are the cache slots of staged rows 0..n-1 and
         ``num_slots`` the cache's slot count, which fixes the key bits compared. The result is
         ``slots`` by increasing slot and the staged row of each (stable). A padding slot
-        (negative) is kept and lands anywhere; the pair scatter skips it. The workspace and the
-        outputs are allocated here, on the current stream of the slots' device, which the sort
-        is enqueued on.
+        (negative) is kept and lands anywhere; the pair scatter skips it. Enqueued on the current
+        stream of the slots' device.
+
+        ``out`` is an optional pair of int64 device tensors of ``slots``'s size to write into;
+        without it they are allocated. The sort's workspace is kept by this object, per device and
+        stream (so calls on different streams never share one), and grows only when a call needs
+        more: repeated calls with ``out`` allocate nothing.
         """
         import torch
 
         sp = _device_ptr(slots, "order_pairs: slots", torch.long)
         n = slots.numel()
         bits = max(1, (int(num_slots) - 1).bit_length())
+        if out is None:
+            out = (torch.empty_like(slots), torch.empty_like(slots))
+        out_slots, out_rows = out
+        for t, what in ((out_slots, "slots_out"), (out_rows, "rows_out")):
+            _device_ptr(t, f"order_pairs: {what}", torch.long)
+            if t.numel() != n:
+                raise RuntimeError(f"order_pairs: {what} holds {t.numel()} entries, not {n}")
+        _one_device("order_pairs", slots, out_slots, out_rows)
         need = ctypes.c_int64()
         with torch.cuda.device(slots.device):
             self._check(self._lib.evs_order_pairs_workspace(n, bits, ctypes.byref(need)))
-            work = torch.empty(max(1, need.value), dtype=torch.uint8, device=slots.device)
-            out_slots = torch.empty_like(slots)
-            out_rows = torch.empty_like(slots)
+            key = (slots.device, _stream_of(slots.device))
+            work = self._workspace.get(key)
+            if work is None or work.numel() < need.value:
+                work = torch.empty(max(1, need.value), dtype=torch.uint8, device=slots.device)
+                self._workspace[key] = work
             self._check(
                 self._lib.evs_order_pairs(sp, n, bits, out_slots.data_ptr(), out_rows.data_ptr(),
                                           work.data_ptr(), work.numel(),

@@ -393,12 +393,18 @@ class StepStager:
         are in flight."""
         step = job.step
         with self._in_flight_lock:
+            # a step whose sink has returned is no longer in flight (a failed one is kept, for
+            # fence() to raise; _check_failed raises it at the next call in any case)
+            for s in [s for s, j in self._in_flight.items() if j.done.is_set() and j.error is None]:
+                del self._in_flight[s]
             oldest = min(self._in_flight) if len(self._in_flight) >= self._depth else None
+            waited = oldest is not None and not self._in_flight[oldest].done.is_set()
         if oldest is not None:
-            self.stats["backpressure_waits"] += 1
             tw = time.perf_counter()
             self.fence(oldest)
-            self.stats["backpressure_s"] += time.perf_counter() - tw
+            if waited:
+                self.stats["backpressure_waits"] += 1
+                self.stats["backpressure_s"] += time.perf_counter() - tw
         with self._in_flight_lock:
             self._in_flight[step] = job
         self._queue.put(job)
@@ -586,29 +592,35 @@ class StepStager:
             self._sink(job)
             return
         try:
-            self._ext.event_synchronize(job.gathered)  # a host wait: no device queue waits
-            job.times["gathered"] = t0 = time.perf_counter()
             st, n = g.stage, g.n
             row_bytes = 2 * self.paged.head_dim * self._kernel.elem
             heads = len(g.heads)
             pitch = st.capacity * row_bytes
             cs = self._copy_stream
             bounce = [b.data_ptr() for b in self._bounce]
+            file_addr, rows_addr = st.file_addr, st.device_rows.data_ptr()
+            runs = ([(0, len(self.layers) * heads)] if len(g.filled) == len(self.layers) else
+                    [(layer * heads * pitch, heads) for layer in sorted(g.filled)])
+            # Everything above is worked out before the wait. The wait ends when the device has
+            # finished the step's forward and gather, the moment the step thread wakes to launch
+            # the next step: from then on this thread goes straight into the delivery, which runs
+            # without the GIL, and does its Python bookkeeping only after it.
+            self._ext.event_synchronize(job.gathered)  # a host wait: no device queue waits
+            t0 = time.perf_counter()
+            for at, count in runs:
+                self._ext.deliver_rows(file_addr + at, pitch, rows_addr + at, pitch, count,
+                                       n * row_bytes, bounce, self._bounce_bytes, cs,
+                                       self._copy_threads)
+            job.times["gathered"] = t0
             with torch.cuda.stream(cs):
-                # the small copies first: the delivery below waits for everything before it
                 self._ext.copy_rows_async(st.host_slots.data_ptr(), st.device_slots.data_ptr(),
                                           1, n * 8, n * 8, self.device)
                 if st.device_scales is not None:
                     nb = st.device_scales.numel() * 4
                     self._ext.copy_rows_async(st.host_scales.data_ptr(),
                                               st.device_scales.data_ptr(), 1, nb, nb, self.device)
-            runs = ([(0, len(self.layers) * heads)] if len(g.filled) == len(self.layers) else
-                    [(layer * heads * pitch, heads) for layer in sorted(g.filled)])
-            file_addr = st.file_addr
-            for at, count in runs:
-                self._ext.deliver_rows(file_addr + at, pitch, st.device_rows.data_ptr() + at,
-                                       pitch, count, n * row_bytes, bounce, self._bounce_bytes,
-                                       cs, self._copy_threads)
+                self._ext.event_record(self._ready, cs)
+            self._ext.event_synchronize(self._ready)
             if st.host_scales is not None:
                 scales = st.host_scales.numpy()
                 np.frombuffer(st.mapping, dtype=np.float32, count=scales.size,

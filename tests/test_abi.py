@@ -81,3 +81,30 @@ def test_the_reduce_state_size_is_the_headers():
     header = (Path(__file__).resolve().parents[1] / "include" / "everserve_mi355x.h").read_text()
     m = re.search(r"#define EVS_REDUCE_STATE_WORDS (\d+)", header)
     assert m is not None and int(m.group(1)) == kernels.REDUCE_STATE_WORDS
+
+
+def test_a_launch_past_the_work_item_limit_is_refused_before_launch(lib):
+    """HIP takes at most 2^32 - 1 work-items along x. C2's shape at 1,048,576 slots over 32 layers
+    is 2^24 gather workgroups of 256 threads, exactly 2^32 work-items: refused with a message,
+    before any device call (this runs without a GPU). 8 slots fewer would be 2^24 - 128
+    workgroups, within the limit."""
+    strides = (ctypes.c_int64 * 5)(16384, 1024, 128, 134217728, 1)
+    fake = ctypes.c_void_p(1 << 20)  # never dereferenced: the call stops at its checks
+    n = 1 << 20
+    rc = lib.evs_gather_rows(fake, 32, fake, n, fake, 8, ctypes.c_void_p(1 << 21), n, 128, 16,
+                             strides, 2, None)
+    assert rc == 1 and b"work-items" in lib.evs_last_error()
+    rc = lib.evs_scatter_rows(fake, 32, fake, 2 * n, fake, 8, ctypes.c_void_p(1 << 21), 2 * n,
+                              128, 16, strides, 2, None)
+    assert rc == 1 and b"work-items" in lib.evs_last_error()
+
+
+def test_failed_parity_flags_fail_the_bench(tmp_path):
+    import bench
+
+    good = {"extra": {"a": {"rows_equal_x": True, "sum_exact": True}, "flag": False}}
+    assert bench.failed_checks(good) == []
+    bad = {"extra": {"c4": {"round_trip_equal_first_4_layers": False},
+                     "s": {"k": {"sum_exact": False}}, "spot_check": False, "rows_check": True}}
+    assert bench.failed_checks(bad) == ["extra.c4.round_trip_equal_first_4_layers",
+                                        "extra.s.k.sum_exact", "extra.spot_check"]

@@ -80,3 +80,25 @@ def test_ordered_on_the_device_then_scattered_equals_the_scatter(ext):
     torch.cuda.synchronize()
     for a, b in zip(layers, want):
         assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+def test_repeated_orderings_into_given_outputs_allocate_nothing(ext):
+    """The workspace is the shim's, kept per device and stream; with outputs given, a second and
+    third call (the third smaller) allocate no device memory and equal a fresh call's result."""
+    rng = np.random.default_rng(5)
+    big = torch.from_numpy(rng.permutation(1 << 16).astype(np.int64)).cuda()
+    small = big[:1000].clone()
+    outs = {n: (torch.empty(n, dtype=torch.long, device="cuda"),
+                torch.empty(n, dtype=torch.long, device="cuda")) for n in (1 << 16, 1000)}
+    ext.order_pairs(big, 1 << 16, out=outs[1 << 16])  # sizes the workspace
+    torch.cuda.synchronize()
+    before = torch.cuda.memory_allocated()
+    for x in (big, small):
+        got = ext.order_pairs(x, 1 << 16, out=outs[x.numel()])
+        torch.cuda.synchronize()
+        assert torch.cuda.memory_allocated() == before
+        want = ext.order_pairs(x.clone(), 1 << 16)
+        assert torch.equal(got[0], want[0]) and torch.equal(got[1], want[1])
+        before = torch.cuda.memory_allocated()
+    with pytest.raises(RuntimeError, match="holds"):
+        ext.order_pairs(small, 1 << 16, out=outs[1 << 16])
