@@ -483,6 +483,9 @@ class StepStager:
         if self._thread.is_alive():
             self._queue.put(None)
             self._thread.join()
+        if self._step is not None:  # layers saved but never committed: their file goes too
+            self._step.stage.release()
+            self._step = None
         with self._pool_lock:
             pool, self._pool = self._pool, []
         for st in pool:

@@ -183,3 +183,14 @@ def test_c3_fp8_share_with_scales_through_the_stager_the_store_and_a_restore(ext
     # the NaN and saturation codes were among the bytes, where a staged block holds them
     codes = layers[0].view(torch.uint8).view(-1)[:256].cpu().numpy()
     assert codes.tolist() == list(range(256))
+
+
+def test_closing_with_a_step_saved_but_not_committed_leaves_no_file(ext, tmp_path):
+    gpu = [t.cuda() for t in caches("kv_first", D, torch.bfloat16, n_layers=2, nb=NB, h=H)]
+    st = staging.StepStager(ext, dict(zip(names(2), gpu)), HEADS, lambda job: None,
+                            rank_dir=tmp_path)
+    sl = torch.tensor([1, 2, 3], dtype=torch.long, device="cuda")
+    st.save(names(2)[0], gpu[0], sl)  # the step's file exists from its first save
+    assert len(os.listdir(tmp_path)) == 1
+    st.close()
+    assert os.listdir(tmp_path) == []
