@@ -1,5 +1,6 @@
 // The library's multi-threaded host entry points under AddressSanitizer or ThreadSanitizer, on
-// the CPU: evs_store_commit on 16 threads, evs_host_gather_ranges on 8, evs_crc32c_rows. Each
+// the CPU: evs_store_commit on 16 threads, evs_host_gather_ranges and evs_host_gather_tables on
+// 8, evs_crc32c_rows. Each
 // result is checked against a plain serial computation here. Built and run by run.sh; host code
 // only (the .hip files hold no kernels this driver calls).
 #include <cstdint>
@@ -13,6 +14,8 @@ int evs_store_commit(const void*, int64_t, const int64_t*, int64_t, void* const*
                      int64_t*);
 int evs_host_gather_ranges(const void*, int64_t, int64_t, const int64_t*, const int64_t*, int64_t,
                            void*, int64_t, int64_t, int64_t*);
+int evs_host_gather_tables(const void* const*, int64_t, int64_t, int64_t, const int64_t*,
+                           const int64_t*, int64_t, void*, int64_t, int64_t, int64_t*);
 int evs_crc32c_rows(const void*, int64_t, int64_t, uint32_t*);
 int evs_crc32c(const void*, int64_t, uint32_t*);
 const char* evs_last_error();
@@ -78,6 +81,30 @@ int main() {
   }
   CHECK(evs_host_gather_ranges(src.data(), SR, RB2, st.data(), ct.data(), st.size(), dst.data(),
                                total - 1, 8, &rows) != 0);
+  // several tables with the same ranges on 8 threads, each into its own block of dst
+  const int64_t NT = 5;
+  std::vector<std::vector<uint8_t>> srcs(NT, std::vector<uint8_t>(SR * RB2 / 8));
+  std::vector<const void*> sp(NT);
+  for (int64_t j = 0; j < NT; j++) {
+    for (auto& b : srcs[j]) b = static_cast<uint8_t>(rng());
+    sp[j] = srcs[j].data();
+  }
+  std::vector<int64_t> st2, ct2;
+  for (int64_t s = 0; s + 40 < SR / 8; s += 53) { st2.push_back(s); ct2.push_back(1 + (s % 40)); }
+  int64_t total2 = 0; for (auto c : ct2) total2 += c;
+  const int64_t room = total2 + 3;
+  std::vector<uint8_t> dst2(NT * room * RB2, 0xEE);
+  CHECK(evs_host_gather_tables(sp.data(), NT, SR / 8, RB2, st2.data(), ct2.data(), st2.size(),
+                               dst2.data(), room, 8, &rows) == 0);
+  CHECK(rows == total2);
+  for (int64_t j = 0; j < NT; j++) {
+    int64_t at2 = 0;
+    for (size_t k = 0; k < st2.size(); k++) {
+      CHECK(std::memcmp(&dst2[(j * room + at2) * RB2], &srcs[j][st2[k] * RB2], ct2[k] * RB2) == 0);
+      at2 += ct2[k];
+    }
+    for (int64_t b = total2 * RB2; b < room * RB2; b++) CHECK(dst2[j * room * RB2 + b] == 0xEE);
+  }
   // crc rows: 4-row interleave and tails
   std::vector<uint32_t> out(1001);
   CHECK(evs_crc32c_rows(src.data(), 77, 1001, out.data()) == 0);
