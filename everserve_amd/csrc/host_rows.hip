@@ -220,8 +220,10 @@ int deliver(char* dst, int64_t dst_pitch, const char* src, int64_t src_pitch, in
   }
   auto issue = [&](size_t i) -> int {
     const Batch& b = batches[i];
+    // one run has no pitch of its own: give the copy its width (the caller's may be smaller)
+    const size_t spitch = static_cast<size_t>(b.nruns > 1 ? src_pitch : b.len);
     EVS_HIP(hipMemcpy2DAsync(bounce[i & 1], static_cast<size_t>(b.len),
-                             src + b.run0 * src_pitch + b.offset, static_cast<size_t>(src_pitch),
+                             src + b.run0 * src_pitch + b.offset, spitch,
                              static_cast<size_t>(b.len), static_cast<size_t>(b.nruns),
                              hipMemcpyDeviceToHost, stream));
     EVS_HIP(hipEventRecord(ev[i & 1], stream));

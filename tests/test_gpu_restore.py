@@ -206,3 +206,63 @@ def test_a_layers_heads_are_scattered_in_one_launch_per_chunk(ext):
     assert np.array_equal(
         oracle.gather_rows(cpu, slots, [3, 2, 1, 0], 128, d, bs, strides_of(cpu[0]), 2),
         oracle.gather_rows(src, slots, [0, 1, 2, 3], 128, d, bs, strides_of(src[0]), 2))
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_restores_equal_the_oracle(ext, seed):
+    """Seeded random restores: layout, head count, block size, layers, written slots committed
+    over several steps (so some tables of a layer differ in their ranges and fall into separate
+    groups), a random head map onto a cache with more head slots, a random chunk size. Every
+    restored head slot equals the source's rows at every written slot, and every other slot of
+    the cache is untouched."""
+    rng = np.random.default_rng(1000 + seed)
+    layout = ["kv_first", "blocks_first", "combined"][seed % 3]
+    nb, bs = int(rng.integers(8, 40)), int(rng.choice([1, 2, 4, 5, 16]))
+    h_src, d = int(rng.integers(1, 5)), int(rng.choice([8, 6, 64]))
+    n_layers = int(rng.integers(1, 4))
+    src = caches(layout, d, torch.bfloat16, n_layers=n_layers, nb=nb, bs=bs, h=h_src,
+                 seed=seed + 7)
+    _, _, _, dd = oracle.recognise(src[0].shape)
+    e = 2
+    held = sorted(rng.choice(h_src, size=int(rng.integers(1, h_src + 1)), replace=False).tolist())
+    tables, written = {}, {}
+    num_slots = nb * bs
+    for step in (1, 2, 3):
+        slots = sorted(rng.choice(num_slots, size=int(rng.integers(1, num_slots // 2 + 2)),
+                                  replace=False).tolist())
+        cap = 1 << max(3, (len(slots) - 1).bit_length())
+        # later steps commit some layers and maybe one head only: a layer's tables then differ
+        # in their written ranges
+        heads = held if step == 1 or rng.random() < 0.5 else held[:1]
+        layers = (list(range(n_layers)) if step == 1 else
+                  sorted(rng.choice(n_layers, size=int(rng.integers(1, n_layers + 1)),
+                                    replace=False).tolist()))
+        rows = oracle.gather_rows(src, slots, heads, cap, dd, bs, strides_of(src[0]), e)
+        desc = oracle.staged_step("s", layers, heads, cap, dd, e, slots, "bfloat16")
+        oracle.store_commit(rows.view(np.uint8).reshape(-1), desc, tables, num_slots, written,
+                            step)
+    h_dst = h_src + int(rng.integers(0, 3))
+    targets = rng.permutation(h_dst)[:len(held)].tolist()
+    moves = dict(zip(held, targets))
+    dst_shape = {"kv_first": (2, nb, bs, h_dst, d), "blocks_first": (nb, 2, bs, h_dst, d),
+                 "combined": (nb, h_dst, bs, 2 * d)}[layout]
+    dst = [torch.zeros(dst_shape, dtype=torch.bfloat16, device="cuda") for _ in range(n_layers)]
+    row_bytes = 2 * d * e
+    chunk = int(rng.integers(1, 64)) * row_bytes
+    r = Restorer(ext, dst, chunk_bytes=chunk, threads=int(rng.integers(1, 5)))
+    tabs = [Table(t, rows, oracle.written_ranges(written[t])) for t, rows in tables.items()]
+    got_rows = r.restore(tabs, moves)
+    assert got_rows == sum(int(written[t].astype(bool).sum()) for t in tables)
+    cpu = [t.cpu() for t in dst]
+    all_slots = list(range(num_slots))
+    for layer in range(n_layers):
+        back = oracle.gather_rows(cpu[layer:layer + 1], all_slots, list(range(h_dst)), num_slots,
+                                  d, bs, strides_of(cpu[0]), e)[0]  # [h_dst, slots, 2, d]
+        want = np.zeros_like(back)
+        for theirs, ours in moves.items():
+            t = layer * 1000 + theirs
+            live = np.flatnonzero(written[t])
+            src_rows = oracle.gather_rows(src[layer:layer + 1], live.tolist(), [theirs],
+                                          max(1, live.size), d, bs, strides_of(src[0]), e)[0, 0]
+            want[ours, live] = src_rows[:live.size]
+        assert np.array_equal(back, want), (layer, moves)

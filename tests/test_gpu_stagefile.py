@@ -36,20 +36,23 @@ pytestmark = pytest.mark.gpu
     (5, 100000, 100032, 4096),      # each run cut into pieces
     (256, 32768, 65536, 32 << 20),  # a decode step's shape: one batch
     (3, 64, 128, 64),               # a run exactly a bounce buffer
+    (1, 4096, 64, 1024),            # one run: its pitch, smaller than the run, is not used
 ])
 def test_deliver_rows_into_memory_that_is_not_pinned(ext, runs, run_bytes, pitch, bounce):
     rng = np.random.default_rng(runs)
-    src = torch.from_numpy(rng.integers(0, 256, size=runs * pitch, dtype=np.uint8)).cuda()
-    dst = np.full(runs * pitch + 64, 0xEE, dtype=np.uint8)  # heap memory, pageable
+    span = max(pitch, run_bytes)
+    src = torch.from_numpy(rng.integers(0, 256, size=runs * span, dtype=np.uint8)).cuda()
+    dst = np.full(runs * span + 64, 0xEE, dtype=np.uint8)  # heap memory, pageable
+    pitch = span if runs > 1 else pitch
     bufs = [torch.empty(bounce, dtype=torch.uint8, pin_memory=True) for _ in range(2)]
     stream = torch.cuda.Stream()
     torch.cuda.synchronize()
     ext.deliver_rows(dst.ctypes.data, pitch, src.data_ptr(), pitch, runs, run_bytes,
                      [b.data_ptr() for b in bufs], bounce, stream, 4)
-    want = src.cpu().numpy().reshape(runs, pitch)
-    got = dst[:runs * pitch].reshape(runs, pitch)
+    want = src.cpu().numpy().reshape(runs, span)
+    got = dst[:runs * span].reshape(runs, span)
     assert np.array_equal(got[:, :run_bytes], want[:, :run_bytes])
-    assert (got[:, run_bytes:] == 0xEE).all() and (dst[runs * pitch:] == 0xEE).all()
+    assert (got[:, run_bytes:] == 0xEE).all() and (dst[runs * span:] == 0xEE).all()
 
 
 def test_deliver_rows_refuses_bad_arguments(ext):
