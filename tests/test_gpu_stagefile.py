@@ -197,3 +197,69 @@ def test_closing_with_a_step_saved_but_not_committed_leaves_no_file(ext, tmp_pat
     assert len(os.listdir(tmp_path)) == 1
     st.close()
     assert os.listdir(tmp_path) == []
+
+
+def _store_process(rank_dir, conn, num_slots):
+    """A store in its own process: it knows the rank directory, maps each staging file by the
+    descriptor's name, commits it (the oracle's restatement of storage.rs:864-957) and answers
+    when done, as the store acknowledges a commit. It never touches the GPU."""
+    import os
+
+    import numpy as np
+
+    import oracle
+
+    tables, written = {}, {}
+    while True:
+        msg = conn.recv()
+        if msg is None:
+            break
+        step_no, desc = msg
+        staged = np.memmap(os.path.join(rank_dir, desc["stage"]), dtype=np.uint8, mode="r")
+        oracle.store_commit(np.asarray(staged), desc, tables, num_slots, written, step_no)
+        del staged
+        conn.send("ok")
+    conn.send({t: (rows.tobytes(), written[t].tobytes()) for t, rows in tables.items()})
+
+
+def test_a_store_in_another_process_maps_the_staging_files_by_name(ext, tmp_path):
+    import multiprocessing as mp
+
+    L = 2
+    cpu = caches("blocks_first", D, torch.bfloat16, n_layers=L, nb=NB, h=H, seed=29)
+    gpu = [t.cuda() for t in cpu]
+    kv = dict(zip(names(L), gpu))
+    ctx = mp.get_context("spawn")
+    here, there = ctx.Pipe()
+    proc = ctx.Process(target=_store_process, args=(str(tmp_path), there, NB * BS))
+    proc.start()
+    steps = [[3, 4, 5, -1], list(range(20, 40)), [63, 0, 1]]
+    try:
+        def sink(job):  # only the descriptor crosses: the rows are in the named file
+            here.send((job.step, job.descriptor))
+            assert here.recv() == "ok"  # the store has taken the step: the file may be reused
+
+        with staging.StepStager(ext, kv, HEADS, sink, depth=1, rank_dir=tmp_path) as st:
+            for k, slots in enumerate(steps, start=1):
+                sl = torch.tensor(slots, dtype=torch.long, device="cuda")
+                for name, t in kv.items():
+                    st.save(name, t, sl)
+                st.commit(1, k, {})
+            st.flush()
+        here.send(None)
+        got = here.recv()
+    finally:
+        proc.join(timeout=60)
+        if proc.is_alive():
+            proc.terminate()
+    want_tables, want_written = {}, {}
+    for k, slots in enumerate(steps, start=1):
+        cap = staging.capacity_for(len(slots))
+        rows = oracle.gather_rows(cpu, slots, HEADS, cap, D, BS, strides_of(cpu[0]), 2)
+        desc = oracle.staged_step("x", range(L), HEADS, cap, D, 2, slots, "bfloat16")
+        oracle.store_commit(rows.view(np.uint8).reshape(-1), desc, want_tables, NB * BS,
+                            want_written, k)
+    assert sorted(got) == sorted(want_tables)
+    for t in want_tables:
+        assert got[t][0] == want_tables[t].tobytes(), t
+        assert got[t][1] == want_written[t].tobytes(), t
