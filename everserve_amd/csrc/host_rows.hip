@@ -17,10 +17,10 @@
 
 #include <algorithm>
 #include <cstring>
-#include <thread>
 #include <vector>
 
 #include "common.hpp"
+#include "workers.hpp"
 
 // 1: the rows are written with nontemporal stores. A plain store first reads every line it
 // writes into the cache (a third stream of host memory traffic beside the table's reads and the
@@ -156,12 +156,11 @@ int gather_tables(const char* name, const void* const* srcs, int64_t num_tables,
                 total);
     return EVS_OK;
   }
-  std::vector<std::thread> pool;
-  pool.reserve(static_cast<size_t>(threads));
-  for (int64_t t = 0; t < threads; t++)
-    pool.emplace_back(copy_tables, s, rows, row_bytes, starts, counts, first_row.data(), nranges,
-                      d, dst_rows, total * t / threads, total * (t + 1) / threads);
-  for (auto& th : pool) th.join();
+  const int64_t* fr = first_row.data();
+  parallel_for(static_cast<int>(threads), [&](int t) {
+    copy_tables(s, rows, row_bytes, starts, counts, fr, nranges, d, dst_rows,
+                total * t / threads, total * (t + 1) / threads);
+  });
   return EVS_OK;
 }
 
@@ -190,15 +189,12 @@ void unpack_parallel(char* dst, int64_t dst_pitch, const char* src, int64_t nrun
     unpack_runs(dst, dst_pitch, src, len, 0, bytes);
     return;
   }
-  std::vector<std::thread> pool;
-  pool.reserve(static_cast<size_t>(threads));
-  for (int64_t t = 0; t < threads; t++) {
+  parallel_for(static_cast<int>(threads), [&](int t) {
     // shares start on 64-byte boundaries of the packed bytes
     const int64_t b0 = (bytes * t / threads) & ~int64_t{63};
     const int64_t b1 = t + 1 == threads ? bytes : (bytes * (t + 1) / threads) & ~int64_t{63};
-    pool.emplace_back(unpack_runs, dst, dst_pitch, src, len, b0, b1);
-  }
-  for (auto& th : pool) th.join();
+    unpack_runs(dst, dst_pitch, src, len, b0, b1);
+  });
 }
 
 // One batch of a delivery: runs [run0, run0 + nruns), bytes [offset, offset + len) of each.

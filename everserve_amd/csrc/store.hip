@@ -12,10 +12,10 @@
 
 #include <algorithm>
 #include <cstring>
-#include <thread>
 #include <vector>
 
 #include "common.hpp"
+#include "workers.hpp"
 
 namespace evs {
 namespace {
@@ -216,13 +216,9 @@ extern "C" int evs_store_commit(const void* stage, int64_t stage_bytes,
   if (threads <= 1) {
     for (int64_t k = 0; k < ntables; k++) one(k);
   } else {
-    std::vector<std::thread> pool;
-    pool.reserve(static_cast<size_t>(threads));
-    for (int64_t t = 0; t < threads; t++)
-      pool.emplace_back([&, t]() {
-        for (int64_t k = t; k < ntables; k += threads) one(k);
-      });
-    for (auto& th : pool) th.join();
+    evs::parallel_for(static_cast<int>(threads), [&](int t) {
+      for (int64_t k = t; k < ntables; k += threads) one(k);
+    });
   }
   if (newly_written != nullptr) {
     int64_t total = 0;

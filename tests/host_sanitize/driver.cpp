@@ -7,6 +7,7 @@
 #include <cstdio>
 #include <cstring>
 #include <random>
+#include <thread>
 #include <vector>
 extern "C" {
 int evs_store_commit(const void*, int64_t, const int64_t*, int64_t, void* const*, uint64_t* const*,
@@ -104,6 +105,26 @@ int main() {
       at2 += ct2[k];
     }
     for (int64_t b = total2 * RB2; b < room * RB2; b++) CHECK(dst2[j * room * RB2 + b] == 0xEE);
+  }
+  // two callers at once: one has the library's worker set, the other runs on threads of its own
+  {
+    std::vector<uint8_t> d1(NT * room * RB2, 0), d2(NT * room * RB2, 0);
+    int64_t r1 = 0, r2 = 0;
+    int rc1 = -1, rc2 = -1;
+    for (int round = 0; round < 20; round++) {
+      std::thread a([&] { rc1 = evs_host_gather_tables(sp.data(), NT, SR / 8, RB2, st2.data(),
+                                                      ct2.data(), st2.size(), d1.data(), room, 8,
+                                                      &r1); });
+      std::thread b([&] { rc2 = evs_host_gather_tables(sp.data(), NT, SR / 8, RB2, st2.data(),
+                                                      ct2.data(), st2.size(), d2.data(), room, 8,
+                                                      &r2); });
+      a.join();
+      b.join();
+      CHECK(rc1 == 0 && rc2 == 0 && r1 == total2 && r2 == total2);
+    }
+    for (int64_t j = 0; j < NT; j++)
+      CHECK(std::memcmp(&d1[j * room * RB2], &dst2[j * room * RB2], total2 * RB2) == 0 &&
+            std::memcmp(&d2[j * room * RB2], &dst2[j * room * RB2], total2 * RB2) == 0);
   }
   // crc rows: 4-row interleave and tails
   std::vector<uint32_t> out(1001);
