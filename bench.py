@@ -1158,8 +1158,9 @@ def pcie_workload(ext, copies=5):
 
     D2H: C3's staged rows, 80 groups of 8 MiB (640 MiB), by ``evs_copy_rows_async`` into pinned
     memory, and by ``evs_deliver_rows`` into a staging file in shared memory (the step path: 32 MiB
-    batches into two pinned bounce buffers). H2D: the restore's 64 MiB chunks by
-    ``evs_copy_rows_async``, 16 of them (1 GiB), and one plain 1 GiB copy. Prints one line of
+    batches into two pinned bounce buffers). H2D: the restore's copies by ``evs_copy_rows_async``,
+    1 GiB in 16 pieces of 64 MiB, each piece 8 head tables' runs of 8 MiB placed 32 MiB apart in
+    a 256 MiB chunk, as the Restorer copies a layer's heads; and one plain 1 GiB copy. Prints one line of
     HIP-event (and, for the delivery, host clock) rates. Every buffer is released before it
     returns, torch's pinned-memory cache included, so nothing of the workload is left for the
     process's exit to tear down.
@@ -1194,9 +1195,14 @@ def pcie_workload(ext, copies=5):
         h.copy_(d, non_blocking=True)
 
     def chunks_h2d():
-        for c in range(chunks):
-            ext.copy_rows_async(d2.data_ptr() + c * chunk, h2.data_ptr() + c * chunk, 1, chunk,
-                                chunk, dev)
+        # a piece is rows [p, p + 8 MiB) of each of 8 tables laid 32 MiB apart in a chunk
+        tables, run = 8, (chunk * 4) // 8 // 4
+        for c in range(chunks // 4):
+            base = c * 4 * chunk
+            for p in range(4):
+                off = base + p * run
+                ext.copy_rows_async(d2.data_ptr() + off, h2.data_ptr() + off, tables, run,
+                                    4 * run, dev)
 
     def plain_h2d():
         d2.copy_(h2, non_blocking=True)

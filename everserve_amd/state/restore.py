@@ -9,17 +9,20 @@ maps it from shared memory as ``[num_slots, 2, d]``, gathers the written rows on
 :class:`Restorer` first checks every table against this rank's cache (its layers, head slots,
 row size and slot count), so a bad table refuses the restore before anything is written. It then
 groups the tables of a layer that share their written ranges (a store commit writes every held
-head of a layer at the same slots) and restores each group in chunks, keeping three things busy
-at once: host threads gathering chunk i+1's rows of all the group's tables side by side into one
-pinned buffer (``evs_host_gather_tables``), the copy engine moving chunk i from the other pinned
-buffer to the device (``evs_copy_rows_async``), and one scatter launch writing chunk i-1 into
-every head slot of the group (``evs_scatter_rows`` with the group's head slots, the layer's own
-strides). Writing all of a layer's heads in one launch covers each cache block's rows whole, in
-increasing slot order. The copies run on a stream of their own, so the copy engine goes from one
-chunk to the next without waiting for the scatter of the previous one; events order each scatter
-after its copy and each copy after the scatter that last read its device buffer. A chunk of one
-slot range gets its slot ids from ``torch.arange`` on the device instead of a second copy. Rows
-land byte for byte where ``write_rows`` puts them.
+head of a layer at the same slots) and restores each group in chunks, one scatter launch a chunk
+(``evs_scatter_rows`` with the group's head slots, the layer's own strides) writing all of the
+group's heads: each cache block's rows are covered whole, in increasing slot order. A chunk
+reaches the device in pieces, which keeps three things busy at once: host threads gathering
+piece i+1's rows of all the group's tables side by side into a pinned buffer
+(``evs_host_gather_tables``), the copy engine moving piece i to the device
+(``evs_copy_rows_async``), and the scatter of the chunk before. Each piece is gathered and copied
+straight into its place in the chunk's ``[tables, rows, 2, d]`` layout, so that the copies can be
+small (the pipeline fills and drains sooner) while the scatters are large (a launch's ramp and
+tail weigh less). The copies run on a stream of their own, so the copy engine goes from one piece
+to the next without waiting for a scatter; events order each scatter after its chunk's copies
+and each chunk's copies after the scatter that last read its device buffer. A chunk of one slot
+range gets its slot ids from ``torch.arange`` on the device instead of a copy. Rows land byte for
+byte where ``write_rows`` puts them.
 """
 
 from __future__ import annotations
@@ -124,20 +127,22 @@ class _Group:
 class Restorer:
     """Writes restored tables into ``layers`` (this rank's caches, in layer order).
 
-    ``chunk_bytes`` is the rows one chunk carries over all of a group's tables; two pinned and
-    two device buffers of this size are allocated once. On MI355X, inside a restore from
-    ``/dev/shm``, a chunk's scatter of 64 MiB ran at 4.9 TB/s and one of 128 MiB at 5.4 (a launch's
-    ramp and tail weigh on the shorter one), but the restore as a whole ran at 55.1 GB/s with 64 MiB
-    chunks and 52.6 with 128: it is bound by the PCIe copies, and a smaller chunk fills and drains
-    the pipeline sooner.
+    ``chunk_bytes`` is the rows one scatter launch writes over all of a group's tables, and
+    ``piece_bytes`` the rows one host gather and one copy to the device carry; two pinned and two
+    device buffers of ``chunk_bytes`` are allocated once. On MI355X, inside a restore from
+    ``/dev/shm``, a scatter of 64 MiB ran at 4.9 TB/s, of 128 MiB at 5.4 and of 256 MiB at 5.7
+    (a launch's ramp and tail weigh on the shorter ones), while the restore as a whole, bound by
+    the PCIe copies, ran 0.5-1 % slower with 256 MiB copies than with 64 MiB ones, which fill and
+    drain the pipeline sooner: hence large chunks of small pieces.
 
     ``scales`` (optional): this rank's per-layer fp32 scale array on the device, ``[L]`` or
     ``[L, k]``, for an fp8 cache; :meth:`restore` writes the scales that travelled beside the rows
     into it. The rows themselves move as raw bytes and are never rescaled.
     """
 
-    def __init__(self, ext, layers: Sequence[torch.Tensor], chunk_bytes: int = 64 << 20,
-                 threads: int | None = None, scales: torch.Tensor | None = None) -> None:
+    def __init__(self, ext, layers: Sequence[torch.Tensor], chunk_bytes: int = 256 << 20,
+                 threads: int | None = None, scales: torch.Tensor | None = None,
+                 piece_bytes: int = 64 << 20) -> None:
         first = layers[0]
         self._ext = ext
         self.layers = list(layers)
@@ -155,6 +160,8 @@ class Restorer:
         self._elem = first.element_size()
         self._row_bytes = 2 * self.paged.head_dim * self._elem
         self._chunk_bytes = max(self._row_bytes, chunk_bytes // self._row_bytes * self._row_bytes)
+        self._piece_bytes = min(self._chunk_bytes, max(self._row_bytes, int(piece_bytes)))
+        self._launches = 0
         self._threads = threads or min(16, len(os.sched_getaffinity(0)))
         self.scales = scales
         if scales is not None and (scales.device != self.device or scales.dtype != torch.float32
@@ -254,6 +261,7 @@ class Restorer:
         stream = torch.cuda.current_stream(self.device)
         total = 0
         buf = 0
+        self._launches = 0
         for g in groups:
             rows, buf = self._restore_group(g, stream, buf)
             total += rows * len(g.tables)
@@ -264,20 +272,30 @@ class Restorer:
         torch.cuda.synchronize(self.device)
         rb = self._row_bytes
         self.timing = {"copy_s": time.perf_counter() - t0, "rows": total, "bytes": total * rb,
-                       "launches": sum(-(-int(g.counts.sum()) // self._rows_per_chunk(g))
-                                       for g in groups)}
+                       "launches": self._launches}
         return total
 
-    def _rows_per_chunk(self, g: _Group) -> int:
-        return max(1, self._chunk_bytes // (len(g.tables) * self._row_bytes))
+    @staticmethod
+    def _ranges(g: _Group, first_row: np.ndarray, r0: int, r1: int) -> tuple[np.ndarray,
+                                                                             np.ndarray]:
+        """The group's ranges trimmed to its rows [r0, r1) (``first_row``: each range's first
+        row in the group's order): (starts, counts)."""
+        k0 = int(np.searchsorted(first_row, r0, side="right")) - 1
+        k1 = int(np.searchsorted(first_row, r1, side="left"))
+        st = g.starts[k0:k1].copy()
+        ct = g.counts[k0:k1].copy()
+        skip = r0 - first_row[k0]
+        st[0] += skip
+        ct[0] -= skip
+        ct[-1] -= first_row[k1] - r1
+        return st, ct
 
     def _restore_group(self, g: _Group, stream, buf: int) -> tuple[int, int]:
         """Enqueue one group's chunks, the first into buffer ``buf``: every table's rows of a
-        slot range gathered on the host side by side, copied to the device, and scattered into
-        all of the group's head slots in one launch. Returns the rows enqueued per table and the
-        buffer the next chunk takes."""
+        slot range gathered on the host side by side and copied to the device, a piece at a time,
+        then scattered into all of the group's head slots in one launch. Returns the rows
+        enqueued per table and the buffer the next chunk takes."""
         rb, k = self._row_bytes, len(g.tables)
-        per = self._rows_per_chunk(g)
         first_row = np.concatenate([[0], np.cumsum(g.counts)])
         rows = int(first_row[-1])
         layer = g.layer
@@ -285,47 +303,48 @@ class Restorer:
         heads = self._head_list(g.heads)
         srcs = [t.rows.ctypes.data for t in g.tables]
         table_rows = g.tables[0].rows.nbytes // rb
-        for c0 in range(0, rows, per):
-            c1 = min(rows, c0 + per)
+        per_chunk = max(1, self._chunk_bytes // (k * rb))
+        per_piece = max(1, self._piece_bytes // (k * rb))
+        for c0 in range(0, rows, per_chunk):
+            c1 = min(rows, c0 + per_chunk)
             n = c1 - c0
-            # the ranges, trimmed to output rows [c0, c1)
-            k0 = int(np.searchsorted(first_row, c0, side="right")) - 1
-            k1 = int(np.searchsorted(first_row, c1, side="left"))
-            st = g.starts[k0:k1].copy()
-            ct = g.counts[k0:k1].copy()
-            skip = c0 - first_row[k0]
-            st[0] += skip
-            ct[0] -= skip
-            ct[-1] -= first_row[k1] - c1
             if self._copied[buf] is not None:
-                self._copied[buf].synchronize()  # the copy out of this pinned buffer is done
-            got = self._ext.host_gather_tables(srcs, table_rows, rb, st, ct,
-                                               self._host[buf].data_ptr(), n, self._threads)
-            if got != n:
-                raise RuntimeError(f"layer {layer}: gathered {got} rows of chunk [{c0}, {c1})")
+                self._copied[buf].synchronize()  # the copies out of this pinned buffer are done
+            host, dev = self._host[buf].data_ptr(), self._dev[buf].data_ptr()
+            # the chunk is [k, n, 2, d]: staged rows of k head slots at capacity n; a piece is
+            # rows [p0, p1) of every table, k runs n rows apart
+            for p0 in range(c0, c1, per_piece):
+                p1 = min(c1, p0 + per_piece)
+                st, ct = self._ranges(g, first_row, p0, p1)
+                off = (p0 - c0) * rb
+                got = self._ext.host_gather_tables(srcs, table_rows, rb, st, ct, host + off, n,
+                                                   self._threads)
+                if got != p1 - p0:
+                    raise RuntimeError(f"layer {layer}: gathered {got} rows of [{p0}, {p1})")
+                with torch.cuda.stream(self._copy_stream):
+                    if p0 == c0 and self._scattered[buf] is not None:
+                        self._copy_stream.wait_event(self._scattered[buf])
+                    self._ext.copy_rows_async(dev + off, host + off, k, (p1 - p0) * rb, n * rb,
+                                              self.device)
+            st, ct = self._ranges(g, first_row, c0, c1)
             one_range = len(st) == 1
-            if not one_range:
-                slots = self._host_slots[buf].numpy()
-                at = 0
-                for s, c in zip(st.tolist(), ct.tolist()):
-                    slots[at:at + c] = np.arange(s, s + c, dtype=np.int64)
-                    at += c
             with torch.cuda.stream(self._copy_stream):
-                if self._scattered[buf] is not None:
-                    self._copy_stream.wait_event(self._scattered[buf])
-                self._ext.copy_rows_async(self._dev[buf].data_ptr(), self._host[buf].data_ptr(),
-                                          1, k * n * rb, k * n * rb, self.device)
                 if not one_range:
+                    slots = self._host_slots[buf].numpy()
+                    at = 0
+                    for s, c in zip(st.tolist(), ct.tolist()):
+                        slots[at:at + c] = np.arange(s, s + c, dtype=np.int64)
+                        at += c
                     self._dev_slots[buf][:n].copy_(self._host_slots[buf][:n], non_blocking=True)
                 self._copied[buf] = self._copy_stream.record_event()
             if one_range:
                 torch.arange(int(st[0]), int(st[0]) + n, dtype=torch.long, device=self.device,
                              out=self._dev_slots[buf][:n])
             stream.wait_event(self._copied[buf])
-            # the chunk is [k, n, 2, d]: staged rows of k head slots at capacity n
-            self._ext.scatter_rows(layer_ptr, self._dev_slots[buf][:n], heads,
-                                   self._dev[buf].data_ptr(), n, self.paged.head_dim,
-                                   self.paged.block_size, self._strides[layer], self._elem)
+            self._ext.scatter_rows(layer_ptr, self._dev_slots[buf][:n], heads, dev, n,
+                                   self.paged.head_dim, self.paged.block_size,
+                                   self._strides[layer], self._elem)
             self._scattered[buf] = stream.record_event()
+            self._launches += 1
             buf ^= 1
         return rows, buf

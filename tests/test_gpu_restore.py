@@ -112,10 +112,12 @@ def test_ranges_outside_a_table_and_partial_rows_are_refused(ext):
     assert not dst[0].any()
 
 
-def test_many_chunks_on_a_side_stream_twice_with_the_same_buffers(ext):
+@pytest.mark.parametrize("piece_rows", [16, 5, 1])
+def test_many_chunks_on_a_side_stream_twice_with_the_same_buffers(ext, piece_rows):
     """Chunks inside one slot range (slot ids made on the device) and across several (slot ids
-    copied), the copies on the Restorer's stream and the scatters on the caller's side stream,
-    and a second restore that reuses the buffers and events of the first."""
+    copied), each reaching the device in pieces (a chunk whole, pieces that do not divide it,
+    one row at a time), the copies on the Restorer's stream and the scatters on the caller's
+    side stream, and a second restore that reuses the buffers and events of the first."""
     nb, bs, h, d = 64, 4, 2, 64
     src = caches("kv_first", d, torch.bfloat16, n_layers=2, nb=nb, bs=bs, h=h, seed=71)
     rng = np.random.default_rng(71)
@@ -125,7 +127,10 @@ def test_many_chunks_on_a_side_stream_twice_with_the_same_buffers(ext):
     ranges = {t: oracle.written_ranges(written[t]) for t in tables}
     assert any(c > 40 for _, c in ranges[0])  # a range longer than a chunk
     dst = [torch.zeros_like(t).cuda() for t in src]
-    r = Restorer(ext, dst, chunk_bytes=16 * 2 * d * 2, threads=2)  # 16 rows a chunk
+    row_bytes = 2 * d * 2
+    # 16 rows of each of the group's 2 tables a chunk
+    r = Restorer(ext, dst, chunk_bytes=2 * 16 * row_bytes, threads=2,
+                 piece_bytes=2 * piece_rows * row_bytes)
     side = torch.cuda.Stream()
     want = oracle.gather_rows(src, slots, [0, 1], len(slots), d, bs, strides_of(src[0]), 2)
     for _ in range(2):
@@ -189,14 +194,16 @@ def test_each_layer_keeps_its_own_strides(ext):
 
 def test_a_layers_heads_are_scattered_in_one_launch_per_chunk(ext):
     """Tables of one layer with the same written ranges form one group: the chunks carry all the
-    group's heads, so the launch count is the chunk count of one table, not of each."""
+    group's heads, so the launch count is the chunk count of one table, not of each, and the
+    pieces a chunk is copied in add no launch."""
     nb, bs, h, d = 32, 4, 4, 8
     src = caches("blocks_first", d, torch.bfloat16, n_layers=3, nb=nb, bs=bs, h=h, seed=64)
     slots = list(range(0, 100))
     tables, written = commit(src, slots, [0, 1, 2, 3], cap=128)
     dst = [torch.zeros_like(t).cuda() for t in src]
     per_chunk_rows = 10
-    r = Restorer(ext, dst, chunk_bytes=4 * per_chunk_rows * 2 * d * 2)
+    r = Restorer(ext, dst, chunk_bytes=4 * per_chunk_rows * 2 * d * 2,
+                 piece_bytes=4 * 3 * 2 * d * 2)
     moves = {0: 3, 1: 2, 2: 1, 3: 0}
     rows = r.restore([Table(t, tb, oracle.written_ranges(written[t])) for t, tb in tables.items()],
                      moves)
@@ -212,7 +219,7 @@ def test_a_layers_heads_are_scattered_in_one_launch_per_chunk(ext):
 def test_random_restores_equal_the_oracle(ext, seed):
     """Seeded random restores: layout, head count, block size, layers, written slots committed
     over several steps (so some tables of a layer differ in their ranges and fall into separate
-    groups), a random head map onto a cache with more head slots, a random chunk size. Every
+    groups), a random head map onto a cache with more head slots, random chunk and piece sizes. Every
     restored head slot equals the source's rows at every written slot, and every other slot of
     the cache is untouched."""
     rng = np.random.default_rng(1000 + seed)
@@ -249,7 +256,8 @@ def test_random_restores_equal_the_oracle(ext, seed):
     dst = [torch.zeros(dst_shape, dtype=torch.bfloat16, device="cuda") for _ in range(n_layers)]
     row_bytes = 2 * d * e
     chunk = int(rng.integers(1, 64)) * row_bytes
-    r = Restorer(ext, dst, chunk_bytes=chunk, threads=int(rng.integers(1, 5)))
+    piece = int(rng.integers(1, 64)) * row_bytes  # pieces past the chunk are a chunk
+    r = Restorer(ext, dst, chunk_bytes=chunk, threads=int(rng.integers(1, 5)), piece_bytes=piece)
     tabs = [Table(t, rows, oracle.written_ranges(written[t])) for t, rows in tables.items()]
     got_rows = r.restore(tabs, moves)
     assert got_rows == sum(int(written[t].astype(bool).sum()) for t in tables)
