@@ -30,7 +30,7 @@ LIBRARY = "libeverserve_mi355x.so"
 STAMP = "stamp.json"
 SOURCES = ("rows.hip", "order.hip", "reduce.hip", "slot.hip", "host_rows.hip", "store.hip",
            "runtime.hip")
-HEADERS = ("common.hpp", "workers.hpp")
+HEADERS = ("common.hpp", "host_copy.hpp", "workers.hpp")
 PUBLIC_HEADERS = ("everserve_mi355x.h",)
 DEFAULT_ARCHS = "gfx950"
 

@@ -20,6 +20,7 @@
 #include <vector>
 
 #include "common.hpp"
+#include "host_copy.hpp"
 #include "workers.hpp"
 
 // 1: the rows are written with nontemporal stores. A plain store first reads every line it
@@ -33,29 +34,6 @@ namespace evs {
 namespace {
 
 constexpr int64_t kMinBytesPerThread = int64_t{4} << 20;  // below this a thread costs more than it copies
-
-typedef long long v2i64 __attribute__((ext_vector_type(2)));
-
-// memcpy with 16-byte nontemporal stores where dst is 16-byte aligned; plain copies for the
-// unaligned head and the tail.
-void stream_copy(char* dst, const char* src, size_t bytes) {
-  size_t head = (16 - (reinterpret_cast<uintptr_t>(dst) & 15)) & 15;
-  if (head > bytes) head = bytes;
-  std::memcpy(dst, src, head);
-  size_t i = head;
-  for (; i + 64 <= bytes; i += 64) {
-    v2i64 w[4];
-    std::memcpy(w, src + i, 64);
-    for (int k = 0; k < 4; k++)
-      __builtin_nontemporal_store(w[k], reinterpret_cast<v2i64*>(dst + i) + k);
-  }
-  for (; i + 16 <= bytes; i += 16) {
-    v2i64 w;
-    std::memcpy(&w, src + i, 16);
-    __builtin_nontemporal_store(w, reinterpret_cast<v2i64*>(dst + i));
-  }
-  std::memcpy(dst + i, src + i, bytes - i);
-}
 
 void copy_bytes(char* dst, const char* src, size_t bytes) {
   if (EVS_HOST_NT_STORES)
@@ -97,7 +75,7 @@ void copy_tables(const char* const* srcs, int64_t rows, int64_t row_bytes, const
     f0 += r1 - r0;
   }
   // nontemporal stores are weakly ordered: drain them before the caller learns the copy is done
-  if (EVS_HOST_NT_STORES) __builtin_ia32_sfence();
+  if (EVS_HOST_NT_STORES) stream_fence();
 }
 
 // Checks every range against the table's rows and dst's room, and fills first_row (the output
@@ -178,7 +156,7 @@ void unpack_runs(char* dst, int64_t dst_pitch, const char* src, int64_t len, int
     copy_bytes(dst + r * dst_pitch + o, src + b0, static_cast<size_t>(take));
     b0 += take;
   }
-  if (EVS_HOST_NT_STORES) __builtin_ia32_sfence();
+  if (EVS_HOST_NT_STORES) stream_fence();
 }
 
 void unpack_parallel(char* dst, int64_t dst_pitch, const char* src, int64_t nruns, int64_t len,

@@ -15,7 +15,21 @@
 #include <vector>
 
 #include "common.hpp"
+#include "host_copy.hpp"
 #include "workers.hpp"
+
+// Steps of at least this many bytes write their table rows with nontemporal stores (see
+// commit_table); smaller ones with memcpy. On the MI355X box's host, a C2 step (256 MiB over 32
+// tables) committed at 55 GB/s on 16 threads with them and 38.7 without, and a 64-slot decode
+// step (1 MiB) in 40 us with them and 30 without (the fence and the partial write-combining
+// lines cost more than the cache misses save at that size).
+#ifndef EVS_STORE_NT_MIN_BYTES
+#define EVS_STORE_NT_MIN_BYTES (int64_t{4} << 20)
+#endif
+// Tables are committed on several threads only when each gets at least this many bytes.
+#ifndef EVS_STORE_MIN_BYTES_PER_THREAD
+#define EVS_STORE_MIN_BYTES_PER_THREAD (int64_t{128} << 10)
+#endif
 
 namespace evs {
 namespace {
@@ -108,12 +122,14 @@ void crc_rows(const uint8_t* const* rows, int64_t count, size_t bytes, uint32_t*
   for (; r < count; r++) out[r] = crc32c(rows[r], bytes);
 }
 
-// One table's commit. Each run of consecutive slots is one copy, and the run's rows are checksummed
-// right after it, while they are still in cache, four at a time. Runs go in order, so a slot named
-// twice keeps the last write's rows, step and checksum, as the store's mark after each copy does.
-// Returns the slots written for the first time.
+// One table's commit. Each run of consecutive slots is checksummed from the staged rows (the bytes
+// it writes), four rows at a time, then copied, with nontemporal stores when `nt`: a large step's
+// slots lie at random places in gigabytes of tables, so a plain store would first miss on every
+// line it writes, where the staged rows are read in order. Runs go in order, so a slot named twice
+// keeps the last write's rows, step and checksum, as the store's mark after each copy does.
+// Returns the slots written for the first time; with `nt` the caller fences the stores.
 int64_t commit_table(const uint8_t* staged, uint8_t* table, uint64_t* written_step, uint32_t* crc,
-                     int64_t row_bytes, const int64_t* slots, int64_t n, uint64_t step) {
+                     int64_t row_bytes, const int64_t* slots, int64_t n, uint64_t step, bool nt) {
   const size_t rb = static_cast<size_t>(row_bytes);
   const uint64_t mark = step > 0 ? step : 1;  // step 0 still counts as written
   int64_t fresh = 0;
@@ -129,11 +145,10 @@ int64_t commit_table(const uint8_t* staged, uint8_t* table, uint64_t* written_st
     }
     int64_t run = 1;
     while (i + run < n && slots[i + run] == s + run) run++;
-    uint8_t* dst = table + static_cast<size_t>(s) * rb;
-    std::memcpy(dst, staged + static_cast<size_t>(i) * rb, static_cast<size_t>(run) * rb);
+    const uint8_t* src = staged + static_cast<size_t>(i) * rb;
     for (int64_t r0 = 0; r0 < run; r0 += kBatch) {
       const int64_t m = std::min(kBatch, run - r0);
-      for (int64_t k = 0; k < m; k++) rows[k] = dst + static_cast<size_t>(r0 + k) * rb;
+      for (int64_t k = 0; k < m; k++) rows[k] = src + static_cast<size_t>(r0 + k) * rb;
       crc_rows(rows, m, rb, sums);
       for (int64_t k = 0; k < m; k++) {
         const int64_t slot = s + r0 + k;
@@ -142,12 +157,17 @@ int64_t commit_table(const uint8_t* staged, uint8_t* table, uint64_t* written_st
         crc[slot] = sums[k];
       }
     }
+    if (nt)
+      stream_copy(reinterpret_cast<char*>(table + static_cast<size_t>(s) * rb),
+                  reinterpret_cast<const char*>(src), static_cast<size_t>(run) * rb);
+    else
+      std::memcpy(table + static_cast<size_t>(s) * rb, src, static_cast<size_t>(run) * rb);
     i += run;
   }
   return fresh;
 }
 
-constexpr int64_t kMinBytesPerThread = int64_t{1} << 20;  // below this a thread costs more
+constexpr int64_t kMinBytesPerThread = EVS_STORE_MIN_BYTES_PER_THREAD;
 
 }  // namespace
 }  // namespace evs
@@ -206,10 +226,12 @@ extern "C" int evs_store_commit(const void* stage, int64_t stage_bytes,
   }
   const uint8_t* st = static_cast<const uint8_t*>(stage);
   std::vector<int64_t> fresh(static_cast<size_t>(ntables), 0);
+  const bool nt = ntables * span >= EVS_STORE_NT_MIN_BYTES;
   auto one = [&](int64_t k) {
     fresh[static_cast<size_t>(k)] =
         evs::commit_table(st + stage_offsets[k], static_cast<uint8_t*>(tables[k]),
-                          written_step[k], crc[k], row_bytes, slots, nslots, step);
+                          written_step[k], crc[k], row_bytes, slots, nslots, step, nt);
+    if (nt) evs::stream_fence();  // this thread's rows are in memory before the commit returns
   };
   int64_t threads = std::min(max_threads, ntables);
   threads = std::min(threads, std::max<int64_t>(1, ntables * span / evs::kMinBytesPerThread));

@@ -28,6 +28,7 @@ import functools
 import json
 import logging
 import os
+from dataclasses import dataclass
 from pathlib import Path
 from typing import Sequence
 
@@ -47,6 +48,20 @@ _PACKAGE = Path(__file__).resolve().parent
 EVS_OK = 0
 REDUCE_STATE_WORDS = 288
 """64-bit words of local_reduce's state record (EVS_REDUCE_STATE_WORDS in the C header)."""
+
+
+@dataclass(frozen=True)
+class CommitPlan:
+    """``evs_store_commit``'s per-table arguments for one set of store tables, built once."""
+
+    T: int
+    offsets: object  # int64 numpy array [T]
+    tables: object  # ctypes void* arrays [T]
+    steps: object
+    crcs: object
+    num_slots: int
+    row_bytes: int
+    keep: tuple  # the arrays the pointers name, kept alive
 
 
 class KernelsUnavailable(RuntimeError):
@@ -508,14 +523,14 @@ class Kernels:
         )
 
     # -------------------------------------------------------------- the store's commit copy
-    def store_commit(self, stage, stage_offsets, tables, written_step, crc, num_slots: int,
-                     row_bytes: int, slots, step: int, max_threads: int = 16) -> int:
-        """Commit one staged step's rows into store tables on host threads; the new slot count.
+    def store_commit_plan(self, stage_offsets, tables, written_step, crc, num_slots: int,
+                          row_bytes: int) -> "CommitPlan":
+        """Check one set of store tables and build ``evs_store_commit``'s arrays for them once,
+        for :meth:`store_commit_with` to commit step after step.
 
-        ``stage`` is a uint8 numpy array (the staged bytes); ``stage_offsets`` int64 [T], where
-        each table's rows start in it; ``tables``, ``written_step`` and ``crc`` are sequences of
-        T numpy arrays: [num_slots * row_bytes] uint8, [num_slots] uint64, [num_slots] uint32.
-        ``slots`` are the step's slot ids (negative: padding). store/src/storage.rs:864-957.
+        ``stage_offsets`` is int64 [T], where each table's rows start in a stage; ``tables``,
+        ``written_step`` and ``crc`` are sequences of T numpy arrays: [num_slots * row_bytes]
+        uint8, [num_slots] uint64, [num_slots] uint32. The plan keeps them alive.
         """
         import numpy as np
 
@@ -530,19 +545,40 @@ class Kernels:
                             and crc[k].flags.c_contiguous)):
                 raise RuntimeError(f"store_commit: table {k}'s arrays do not match "
                                    f"{num_slots} slots of {row_bytes} bytes")
+        return CommitPlan(
+            T, np.ascontiguousarray(stage_offsets, dtype=np.int64),
+            (ctypes.c_void_p * max(T, 1))(*[t.ctypes.data for t in tables]),
+            (ctypes.c_void_p * max(T, 1))(*[w.ctypes.data for w in written_step]),
+            (ctypes.c_void_p * max(T, 1))(*[c.ctypes.data for c in crc]),
+            int(num_slots), int(row_bytes), (list(tables), list(written_step), list(crc)))
+
+    def store_commit_with(self, plan: "CommitPlan", stage, slots, step: int,
+                          max_threads: int = 16) -> int:
+        """Commit one staged step's rows into a plan's tables on host threads; the new slot
+        count. ``stage`` is a contiguous uint8 numpy array (the staged bytes), ``slots`` the
+        step's slot ids (negative: padding). store/src/storage.rs:864-957."""
+        import numpy as np
+
         if stage.dtype != np.uint8 or not stage.flags.c_contiguous:
             raise RuntimeError("store_commit: the stage is contiguous uint8")
-        offs = np.ascontiguousarray(stage_offsets, dtype=np.int64)
         sl = np.ascontiguousarray(slots, dtype=np.int64)
-        ptrs = (ctypes.c_void_p * max(T, 1))(*[t.ctypes.data for t in tables])
-        steps = (ctypes.c_void_p * max(T, 1))(*[w.ctypes.data for w in written_step])
-        crcs = (ctypes.c_void_p * max(T, 1))(*[c.ctypes.data for c in crc])
         fresh = ctypes.c_int64()
         self._check(self._lib.evs_store_commit(
-            stage.ctypes.data, stage.size, offs.ctypes.data, T, ptrs, steps, crcs,
-            int(num_slots), int(row_bytes), sl.ctypes.data, sl.size, int(step) & (2**64 - 1),
-            int(max_threads), ctypes.byref(fresh)))
+            stage.ctypes.data, stage.size, plan.offsets.ctypes.data, plan.T, plan.tables,
+            plan.steps, plan.crcs, plan.num_slots, plan.row_bytes, sl.ctypes.data, sl.size,
+            int(step) & (2**64 - 1), int(max_threads), ctypes.byref(fresh)))
         return fresh.value
+
+    def store_commit(self, stage, stage_offsets, tables, written_step, crc, num_slots: int,
+                     row_bytes: int, slots, step: int, max_threads: int = 16) -> int:
+        """Commit one staged step's rows into store tables on host threads; the new slot count.
+
+        :meth:`store_commit_plan` and :meth:`store_commit_with` in one call (arguments as
+        there). store/src/storage.rs:864-957.
+        """
+        plan = self.store_commit_plan(stage_offsets, tables, written_step, crc, num_slots,
+                                      row_bytes)
+        return self.store_commit_with(plan, stage, slots, step, max_threads)
 
     def crc32c(self, data) -> int:
         """CRC32C (Castagnoli) of a bytes-like object or a contiguous numpy array."""

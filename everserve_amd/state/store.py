@@ -98,6 +98,9 @@ class StoreTables:
         self.step = 0
         self.scales: np.ndarray | None = None
         """The per-layer scales of the latest step that carried them."""
+        self._plans: dict[tuple, object] = {}
+        """Per table set a descriptor names, the commit's arguments built once (tables are
+        never replaced once created)."""
 
     def _create(self, table: int, row_bytes: int) -> StoreTable:
         nbytes = self.num_slots * row_bytes
@@ -121,20 +124,25 @@ class StoreTables:
         """
         stage = np.ascontiguousarray(stage).view(np.uint8).reshape(-1)
         rb = row_bytes_of(step)
-        tables = derive(step)
-        for table, _ in tables:
-            have = self.tables.get(table)
-            if have is not None and have.row_bytes != rb:
-                raise ValueError(f"table {table} holds rows of {have.row_bytes} bytes, the step "
-                                 f"names {rb}")
+        key = (tuple(step["layers"]), tuple(step["heads"]), int(step["table_stride"]),
+               int(step["base_offset"]), int(step["layer_stride"]), int(step["head_stride"]), rb)
+        plan = self._plans.get(key)
+        if plan is None:
+            tables = derive(step)
+            for table, _ in tables:
+                have = self.tables.get(table)
+                if have is not None and have.row_bytes != rb:
+                    raise ValueError(f"table {table} holds rows of {have.row_bytes} bytes, the "
+                                     f"step names {rb}")
         slots = np.asarray(step["slots"], dtype=np.int64)
         if slots.size and int(slots.max()) >= self.num_slots:
             raise ValueError(f"slot {int(slots.max())} outside 0..{self.num_slots}")
-        made = [self.tables.get(t) or self._create(t, rb) for t, _ in tables]
-        fresh = self._ext.store_commit(
-            stage, [off for _, off in tables], [t.rows for t in made],
-            [t.written_step for t in made], [t.crc for t in made], self.num_slots, rb, slots,
-            step_no, self.threads)
+        if plan is None:
+            made = [self.tables.get(t) or self._create(t, rb) for t, _ in tables]
+            plan = self._plans[key] = self._ext.store_commit_plan(
+                [off for _, off in tables], [t.rows for t in made],
+                [t.written_step for t in made], [t.crc for t in made], self.num_slots, rb)
+        fresh = self._ext.store_commit_with(plan, stage, slots, step_no, self.threads)
         self.step = max(self.step, int(step_no))
         return fresh
 

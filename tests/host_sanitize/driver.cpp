@@ -29,40 +29,43 @@ static int fails = 0;
 
 int main() {
   std::mt19937_64 rng(7);
-  // store commit: 16 tables x 8192 slots x 512 B, a step of 4096 slots (runs, padding, a repeat)
-  const int64_t T = 16, S = 8192, RB = 512, N = 4096;
-  std::vector<int64_t> slots(N);
-  for (int64_t i = 0; i < N; i++) slots[i] = (i / 16) * 32 + (i % 16);  // runs of 16, gaps
-  for (int64_t i = 0; i < N; i += 97) slots[i] = -1;
-  std::vector<uint8_t> stage(T * N * RB);
-  for (auto& b : stage) b = static_cast<uint8_t>(rng());
-  std::vector<int64_t> offs(T);
-  for (int64_t k = 0; k < T; k++) offs[k] = k * N * RB;
-  std::vector<std::vector<uint8_t>> tab(T, std::vector<uint8_t>(S * RB));
-  std::vector<std::vector<uint64_t>> ws(T, std::vector<uint64_t>(S));
-  std::vector<std::vector<uint32_t>> crc(T, std::vector<uint32_t>(S));
-  std::vector<void*> tp(T); std::vector<uint64_t*> wp(T); std::vector<uint32_t*> cp(T);
-  for (int64_t k = 0; k < T; k++) { tp[k] = tab[k].data(); wp[k] = ws[k].data(); cp[k] = crc[k].data(); }
-  int64_t fresh = -1;
-  int rc = evs_store_commit(stage.data(), stage.size(), offs.data(), T, tp.data(), wp.data(), cp.data(),
-                            S, RB, slots.data(), N, 5, 16, &fresh);
-  CHECK(rc == 0);
-  int64_t want_fresh = 0;
-  for (int64_t k = 0; k < T; k++)
-    for (int64_t i = 0; i < N; i++) {
-      if (slots[i] < 0) continue;
-      CHECK(std::memcmp(&tab[k][slots[i] * RB], &stage[offs[k] + i * RB], RB) == 0);
-      CHECK(ws[k][slots[i]] == 5);
-      uint32_t c; evs_crc32c(&tab[k][slots[i] * RB], RB, &c);
-      CHECK(crc[k][slots[i]] == c);
-    }
-  for (int64_t i = 0; i < N; i++) want_fresh += slots[i] >= 0;
-  CHECK(fresh == want_fresh * T);
-  // a bad slot is refused before anything is written
-  std::vector<int64_t> bad = slots; bad[N - 1] = S;
-  CHECK(evs_store_commit(stage.data(), stage.size(), offs.data(), T, tp.data(), wp.data(), cp.data(),
-                         S, RB, bad.data(), N, 6, 16, &fresh) != 0);
-  CHECK(ws[0][slots[1]] == 5);
+  // store commit: 16 tables x 8192 slots x 512 B, a step of 4096 slots (32 MiB: nontemporal
+  // stores) and one of 256 (2 MiB: memcpy, still 16 threads), with runs, padding and a repeat
+  for (const int64_t N : {int64_t{4096}, int64_t{256}}) {
+    const int64_t T = 16, S = 8192, RB = 512;
+    std::vector<int64_t> slots(N);
+    for (int64_t i = 0; i < N; i++) slots[i] = (i / 16) * 32 + (i % 16);  // runs of 16, gaps
+    for (int64_t i = 0; i < N; i += 97) slots[i] = -1;
+    std::vector<uint8_t> stage(T * N * RB);
+    for (auto& b : stage) b = static_cast<uint8_t>(rng());
+    std::vector<int64_t> offs(T);
+    for (int64_t k = 0; k < T; k++) offs[k] = k * N * RB;
+    std::vector<std::vector<uint8_t>> tab(T, std::vector<uint8_t>(S * RB));
+    std::vector<std::vector<uint64_t>> ws(T, std::vector<uint64_t>(S));
+    std::vector<std::vector<uint32_t>> crc(T, std::vector<uint32_t>(S));
+    std::vector<void*> tp(T); std::vector<uint64_t*> wp(T); std::vector<uint32_t*> cp(T);
+    for (int64_t k = 0; k < T; k++) { tp[k] = tab[k].data(); wp[k] = ws[k].data(); cp[k] = crc[k].data(); }
+    int64_t fresh = -1;
+    int rc = evs_store_commit(stage.data(), stage.size(), offs.data(), T, tp.data(), wp.data(),
+                              cp.data(), S, RB, slots.data(), N, 5, 16, &fresh);
+    CHECK(rc == 0);
+    int64_t want_fresh = 0;
+    for (int64_t k = 0; k < T; k++)
+      for (int64_t i = 0; i < N; i++) {
+        if (slots[i] < 0) continue;
+        CHECK(std::memcmp(&tab[k][slots[i] * RB], &stage[offs[k] + i * RB], RB) == 0);
+        CHECK(ws[k][slots[i]] == 5);
+        uint32_t c; evs_crc32c(&tab[k][slots[i] * RB], RB, &c);
+        CHECK(crc[k][slots[i]] == c);
+      }
+    for (int64_t i = 0; i < N; i++) want_fresh += slots[i] >= 0;
+    CHECK(fresh == want_fresh * T);
+    // a bad slot is refused before anything is written
+    std::vector<int64_t> bad = slots; bad[N - 1] = S;
+    CHECK(evs_store_commit(stage.data(), stage.size(), offs.data(), T, tp.data(), wp.data(),
+                           cp.data(), S, RB, bad.data(), N, 6, 16, &fresh) != 0);
+    CHECK(ws[0][slots[1]] == 5);
+  }
   // host gather: 64 MiB of ranges on 8 threads
   const int64_t SR = 262144, RB2 = 256;
   std::vector<uint8_t> src(SR * RB2);
