@@ -116,6 +116,48 @@ def test_the_commit_is_the_stores(ext, threads):
     assert ours["steps"][3002][88] == 1  # step 0 counts as written: recorded as 1
 
 
+@pytest.mark.parametrize("threads", [1, 16])
+def test_a_large_step_written_with_streaming_stores_is_the_stores(ext, threads):
+    """A step of 4 MiB or more takes the commit's other copy (nontemporal stores): 4 tables of
+    2,048 rows of 512 B, ascending runs, padding and a repeated slot, then a small step into the
+    same tables."""
+    num_slots, d, elem = 4096, 128, 2
+    ours = {"rows": {}, "steps": {}, "crc": {}}
+    theirs = {"rows": {}, "steps": {}, "crc": {}}
+    rng = np.random.default_rng(11)
+    slots = rng.permutation(num_slots)[:2048].tolist()
+    slots[5], slots[99] = -1, slots[98]
+    stage, desc = staged([0, 1], [0, 1], 2048, d, elem, slots, seed=12)
+    assert stage.nbytes >= 4 << 20
+    commit_both(ext, stage, desc, num_slots, 4, threads, (ours, theirs))
+    stage, desc = staged([0, 1], [0, 1], 8, d, elem, [7, 8, 9, slots[0]], seed=13)
+    commit_both(ext, stage, desc, num_slots, 5, threads, (ours, theirs))
+    for t in theirs["rows"]:
+        assert np.array_equal(ours["rows"][t], theirs["rows"][t]), t
+        assert np.array_equal(ours["steps"][t], theirs["steps"][t]), t
+        assert np.array_equal(ours["crc"][t], theirs["crc"][t]), t
+
+
+def test_store_tables_reuse_a_table_sets_commit_arguments(ext):
+    """Steps that name a table set, another one with a new table, and the first again (its
+    arguments built before are used): every table equals the oracle's after each step."""
+    num_slots, d = 64, 8
+    store = StoreTables(ext, num_slots, threads=2)
+    tables, written, crcs = {}, {}, {}
+    for step, (layers, heads, slots) in enumerate((([0, 1], [0], [1, 2, 3]),
+                                                   ([1, 2], [0, 1], [4, 5, -1]),
+                                                   ([0, 1], [0], [6, 1]),
+                                                   ([1, 2], [0, 1], [7])), start=1):
+        stage, desc = staged(layers, heads, 8, d, 2, slots, seed=20 + step)
+        store.commit(stage, desc, step)
+        oracle.store_commit(stage, desc, tables, num_slots, written, step, crcs)
+        assert sorted(store.tables) == sorted(tables)
+        for t, want in tables.items():
+            assert np.array_equal(np.asarray(store.tables[t].rows), want), (step, t)
+            assert np.array_equal(store.tables[t].crc, crcs[t]), (step, t)
+    assert len(store._plans) == 2
+
+
 def test_a_bad_step_is_refused_before_anything_is_written(ext):
     num_slots, d = 32, 8
     stage, desc = staged([0], [0, 1], 8, d, 2, [3, 4, 40], seed=1)
