@@ -159,7 +159,11 @@ class Restorer:
         self._strides = [list(g.layout_strides(t)) for t, g in zip(layers, self._geometry)]
         self._elem = first.element_size()
         self._row_bytes = 2 * self.paged.head_dim * self._elem
-        self._chunk_bytes = max(self._row_bytes, chunk_bytes // self._row_bytes * self._row_bytes)
+        # a chunk carries at least one row of each of a group's tables, and a group has at most
+        # one table per head slot
+        most_heads = max(g.num_heads for g in self._geometry)
+        self._chunk_bytes = max(most_heads * self._row_bytes,
+                                chunk_bytes // self._row_bytes * self._row_bytes)
         self._piece_bytes = min(self._chunk_bytes, max(self._row_bytes, int(piece_bytes)))
         self._launches = 0
         self._threads = threads or min(16, len(os.sched_getaffinity(0)))
@@ -305,6 +309,9 @@ class Restorer:
         table_rows = g.tables[0].rows.nbytes // rb
         per_chunk = max(1, self._chunk_bytes // (k * rb))
         per_piece = max(1, self._piece_bytes // (k * rb))
+        if k * per_chunk * rb > self._chunk_bytes:
+            raise RuntimeError(f"layer {layer}: a chunk of {k} tables x {per_chunk} rows does "
+                               f"not fit the {self._chunk_bytes}-byte buffers")
         for c0 in range(0, rows, per_chunk):
             c1 = min(rows, c0 + per_chunk)
             n = c1 - c0

@@ -145,6 +145,28 @@ def test_many_chunks_on_a_side_stream_twice_with_the_same_buffers(ext, piece_row
         assert np.array_equal(got, want)
 
 
+@pytest.mark.parametrize("chunk_bytes", [1, 32, 3 * 32])
+def test_a_chunk_smaller_than_a_row_of_every_table_still_holds_one(ext, chunk_bytes):
+    """A chunk carries at least one row of each of a group's tables: with a chunk of one row or
+    less and 4 head tables a group, the buffers hold 4 rows, and the restore equals the
+    oracle's rows."""
+    nb, bs, h, d = 8, 4, 4, 8
+    src = caches("kv_first", d, torch.bfloat16, n_layers=1, nb=nb, bs=bs, h=h, seed=83)
+    slots = [0, 1, 2, 5, 9, 10, 30]
+    tables, written = commit(src, slots, [0, 1, 2, 3], cap=8)
+    dst = [torch.zeros_like(t).cuda() for t in src]
+    r = Restorer(ext, dst, chunk_bytes=chunk_bytes, piece_bytes=1)
+    moves = {0: 2, 1: 3, 2: 0, 3: 1}
+    rows = r.restore([Table(t, tb, oracle.written_ranges(written[t])) for t, tb in tables.items()],
+                     moves)
+    assert rows == len(slots) * 4
+    assert r.timing["launches"] == len(slots)  # a chunk of one row of each of the 4 tables
+    cpu = dst[0].cpu()
+    got = oracle.gather_rows([cpu], slots, [2, 3, 0, 1], 8, d, bs, strides_of(cpu), 2)
+    want = oracle.gather_rows([src[0]], slots, [0, 1, 2, 3], 8, d, bs, strides_of(src[0]), 2)
+    assert np.array_equal(got, want)
+
+
 def test_tables_that_do_not_fit_this_ranks_cache_are_refused_before_anything_is_written(ext):
     """A table of a layer this rank lacks, a head slot past the layer's heads, a written range
     past the cache's slots (a table of a larger cache), rows of another size, or two tables into
