@@ -11,7 +11,8 @@ commit. The other cases are:
 * a later step of another size, on a pooled buffer of another capacity;
 * a cache that the next "forward" changes on the same stream straight after the commit (the
   rows staged are the ones before the change);
-* a sink that fails, which surfaces on the step thread.
+* a sink that fails, which surfaces on the step thread;
+* save and commit never reading device memory or waiting on the device on the step thread.
 
 Each step's descriptor is also checked against the oracle's.
 """
@@ -108,6 +109,53 @@ def test_steps_land_in_the_store_as_the_oracle_puts_them(ext):
         cap = staging.capacity_for(len(slots))
         ref = oracle.staged_step(desc["stage"], layers, HEADS, cap, D, 2, slots, "bfloat16")
         assert desc == ref
+
+
+def test_save_and_commit_never_read_device_memory_on_the_step_thread(ext, monkeypatch):
+    """The reference's rule (core/tests/test_mirror_client.py:345-375): reading a tensor on the
+    host from the step thread drains the GPU, a forward pass paid inside commit(). Every host-side
+    read of a tensor (cpu, tolist, item, numpy, bool) and every host wait on the device
+    (torch.cuda.synchronize, a stream's or event's synchronize, the library's event wait) is
+    forbidden on the step thread while steps and a block round are saved and committed; the copy
+    thread does all of them. The sink still gets every step, padding ids included."""
+    L = 2
+    gpu = [t.cuda() for t in caches("kv_first", D, torch.bfloat16, n_layers=L, nb=NB, h=H,
+                                    seed=29)]
+    kv = dict(zip(names(L), gpu))
+    store = Store()
+    st = staging.StepStager(ext, kv, HEADS, store, depth=2)
+    steps = [[3, 9, -1], list(range(20, 33)), [0, 63]]
+    slot_tensors = [torch.tensor(s, dtype=torch.long, device="cuda") for s in steps]
+    torch.cuda.synchronize()
+    step_thread = threading.current_thread()
+
+    def forbid(owner, name):
+        real = getattr(owner, name)
+
+        def guarded(*args, **kwargs):
+            if threading.current_thread() is step_thread:
+                raise AssertionError(f"{name} on the step thread")
+            return real(*args, **kwargs)
+
+        monkeypatch.setattr(owner, name, guarded)
+
+    for name in ("cpu", "tolist", "item", "numpy", "__bool__"):
+        forbid(torch.Tensor, name)
+    forbid(torch.cuda, "synchronize")
+    forbid(torch.cuda.Stream, "synchronize")
+    forbid(torch.cuda.Event, "synchronize")
+    forbid(ext, "event_synchronize")
+    for step_no, sl in enumerate(slot_tensors, start=1):
+        for name, t in kv.items():
+            st.save(name, t, sl)
+        st.commit(epoch=1, step=step_no, committed_tokens={"r": step_no})
+    st.commit_blocks(epoch=1, step=len(steps) + 1, block_ids=[5, 2])
+    st.flush()
+    monkeypatch.undo()
+    st.close()
+    got = {step: desc["slots"] for step, desc in store.descriptors}
+    assert got == {1: steps[0], 2: steps[1], 3: steps[2],
+                   4: [5 * BS + i for i in range(BS)] + [2 * BS + i for i in range(BS)]}
 
 
 def test_the_llama_shaped_decode_step(ext):
