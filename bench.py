@@ -971,12 +971,15 @@ def bench_decode_overhead(ext, steps, warmup):
     F = torch.nn.functional
     w = []
     for _ in range(Lyr):
-        # weights stored [out, in], as nn.Linear keeps them; K and V [seq x kv head, 1, ctx, d]
+        # weights stored [out, in], as nn.Linear keeps them; K and V [seq x kv head, 1, ctx, d].
+        # The proxy has no norms, so its MLP (quadratic in x) is scaled down to keep the
+        # residual stream finite over 32 layers (largest |x| about 60); what a GEMM costs does
+        # not depend on the values.
         w.append({
             "qkv": torch.randn((HQ + 2 * HKV) * DH, Hd, device=dev, dtype=bf) * 0.02,
             "o": torch.randn(Hd, HQ * DH, device=dev, dtype=bf) * 0.02,
             "up": torch.randn(2 * FF, Hd, device=dev, dtype=bf) * 0.02,
-            "down": torch.randn(Hd, FF, device=dev, dtype=bf) * 0.02,
+            "down": torch.randn(Hd, FF, device=dev, dtype=bf) * 2e-5,
             "k": torch.randn(B * HKV, 1, CTX, DH, device=dev, dtype=bf),
             "v": torch.randn(B * HKV, 1, CTX, DH, device=dev, dtype=bf),
         })
@@ -1019,7 +1022,10 @@ def bench_decode_overhead(ext, steps, warmup):
         return g, o
 
     graph, out = capture(forward)
-    graph_equal = bool(torch.equal(out, eager_out))
+    # the library GEMMs may pick other algorithms inside a capture, so the graph's output can
+    # differ from the eager one in the last bits; a capture that went wrong differs by O(1)
+    graph_rel = float((out.float() - eager_out.float()).abs().max()
+                      / eager_out.float().abs().max().clamp_min(1e-30))
     # the same step with fp8-e4m3 weights (per-tensor scale 1), as an FP8 checkpoint is served;
     # the activations are cast to fp8 per GEMM and the KV cache stays bf16
     fp8 = torch.float8_e4m3fn
@@ -1129,7 +1135,8 @@ def bench_decode_overhead(ext, steps, warmup):
         "proxy_bytes_per_step": step_bytes,
         "proxy_hbm_gbs": round(step_bytes / off / 1e9, 1),
         "eager_forward_ms": round(sorted(eager_ms)[1], 3),
-        "graph_forward_bitwise_same": graph_equal,
+        "graph_forward_max_rel_diff": round(graph_rel, 6),
+        "graph_forward_close_ok": graph_rel < 5e-2,
         "step_thread_us_per_step": round((st["step_thread_s"] - st["backpressure_s"]) /
                                          max(1, st["steps"]) * 1e6, 2),
         "copy_thread_us_per_step": round(st["copy_s"] / max(1, st["steps"]) * 1e6, 2),
