@@ -101,6 +101,14 @@ constexpr uint32_t kXcds = 8;
 #ifndef EVS_PAIRS_VPT
 #define EVS_PAIRS_VPT 2
 #endif
+// The scatter of written ranges (staged rows to the slots of (start, count) ranges, which ascend
+// in a restore): each XCD takes one contiguous part of the grid (chunk -1), so that the XCDs write
+// the cache in 8 streams that each run front to back. On a restore's chunk (1 layer, 8 heads,
+// 65,536 ascending slots, 256 MiB of rows) that measured 6,339 GB/s against 5,735 for the slot
+// scatter's chunk of 64, isolated launches.
+#ifndef EVS_RANGES_XCD_CHUNK
+#define EVS_RANGES_XCD_CHUNK -1
+#endif
 // Tile shape per direction: words a tile aims at, heads it covers (0: all), head groups fastest.
 #ifndef EVS_GATHER_TILE_WORDS
 #define EVS_GATHER_TILE_WORDS 512
@@ -127,8 +135,9 @@ constexpr int kMaxHeads = 256;      // LDS table of head offsets
 enum Dir : int { kGather = 0, kScatter = 1 };
 // kBySlots: row t of a layer's staging goes to (or comes from) slot slots[t]; kByBlocks: row t is
 // offset t % bs of the (t / bs)-th listed block; kByPairs (scatter): staged row rows_of[i] goes
-// to slot slots[i].
-enum Index : int { kBySlots = 0, kByBlocks = 1, kByPairs = 2 };
+// to slot slots[i]; kByRanges (scatter): row t goes to slot starts[k] + t - first_rows[k] of the
+// range k with first_rows[k] <= t < first_rows[k + 1].
+enum Index : int { kBySlots = 0, kByBlocks = 1, kByPairs = 2, kByRanges = 3 };
 
 constexpr int threads_of(int d, int i) {
   return i == kByPairs ? EVS_PAIRS_THREADS : d == kGather ? EVS_GATHER_THREADS : EVS_SCATTER_THREADS;
@@ -172,6 +181,9 @@ struct RowsArgs {
   char* rows;                 // the staging buffer, [L, H, cap, 2, d]
   int64_t* slots_out;         // kByBlocks: the expanded slot ids, or null
   const int64_t* rows_of;     // kByPairs: the staged row of each listed slot
+  const int64_t* starts;      // kByRanges: device, each range's first slot
+  const int64_t* first_rows;  // kByRanges: device, each range's first row, then n
+  int64_t nranges;            // kByRanges
   int64_t n;                  // slots moved per layer
   int64_t cap;                // staging capacity (rows per (layer, head))
   int64_t half_bytes;         // d * elem
@@ -260,6 +272,22 @@ __device__ __forceinline__ TileId tile_id(const RowsArgs& a, uint32_t b) {
   return id;
 }
 
+// The slot of staged row t (0 <= t < n) in the written ranges: the last range k whose first row
+// is at most t, found by bisection over first_rows (ascending, first_rows[0] = 0, the last entry
+// n), so an empty range is passed over. Ranges that break these rules give slots the caller did
+// not mean, as wrong slot ids would; a negative one moves nothing.
+__device__ __forceinline__ int64_t slot_in_ranges(const RowsArgs& a, int64_t t) {
+  int64_t lo = 0, hi = a.nranges;
+  while (hi - lo > 1) {
+    const int64_t mid = (lo + hi) >> 1;
+    if (a.first_rows[mid] <= t)
+      lo = mid;
+    else
+      hi = mid;
+  }
+  return a.starts[lo] + (t - a.first_rows[lo]);
+}
+
 // The index entry row t of a layer needs: its slot id, or in the block-table path its block's id.
 // It is read at a clamped position (n >= 1 here), so that the read needs no branch; the caller
 // discards what it read for a row past n.
@@ -267,6 +295,7 @@ template <int I>
 __device__ __forceinline__ int64_t index_entry(const RowsArgs& a, int64_t t) {
   const int64_t tc = t < a.n ? t : a.n - 1;
   if (I == kByBlocks) return a.blocks[block_of(tc, a)];
+  if (I == kByRanges) return slot_in_ranges(a, tc);
   return a.slots[tc];
 }
 
@@ -381,12 +410,13 @@ __device__ __forceinline__ void tile_offsets(const RowsArgs& a, const TileId& id
   const int h0 = static_cast<int>(id.group) * a.HG;
   if (tid < kMaxTileSlots) {
     const int64_t t = t0 + (tid < a.TS ? tid : a.TS - 1);
-    const int64_t entry = index_entry<I == kByPairs ? kBySlots : I>(a, t);
+    const int64_t entry = index_entry<I == kByPairs ? kBySlots : I>(a, t);  // a slot, or a block
     const int64_t src = I == kByPairs ? a.rows_of[t < a.n ? t : a.n - 1] : 0;
     const int hc = h0 + (tid < a.HG ? tid : a.HG - 1);
     const int64_t head = a.heads[hc < a.H ? hc : a.H - 1];
     if (tid < a.TS) {
-      int64_t off = slot_offset<D, I == kByPairs ? kBySlots : I>(a, id.layer, t0 + tid, entry);
+      int64_t off = slot_offset<D, I == kByBlocks ? kByBlocks : kBySlots>(a, id.layer, t0 + tid,
+                                                                          entry);
       if (I == kByPairs) {
         if (src < 0 || src >= a.cap) off = -1;  // a staged row outside the buffer moves nothing
         s_src[tid] = src;
@@ -434,6 +464,9 @@ struct RowsCall {
   int64_t* slots_out;
   const int64_t* rows_of;
   hipStream_t stream;
+  const int64_t* starts = nullptr;      // kByRanges
+  const int64_t* first_rows = nullptr;  // kByRanges
+  int64_t nranges = 0;                  // kByRanges
 };
 
 template <int D, int I, typename T>
@@ -445,6 +478,7 @@ int launch_typed(RowsArgs a, int64_t L, uint32_t W, hipStream_t stream, const ch
   a.HG = (hpt > 0 && hpt < a.H) ? hpt : a.H;
   a.group_fastest = D == kGather ? EVS_GATHER_GROUP_FASTEST : EVS_SCATTER_GROUP_FASTEST;
   a.xcd_chunk = I == kByPairs ? EVS_PAIRS_XCD_CHUNK
+                : I == kByRanges ? EVS_RANGES_XCD_CHUNK
                 : D == kGather ? EVS_GATHER_XCD_CHUNK : EVS_SCATTER_XCD_CHUNK;
   const int64_t groups = (a.H + a.HG - 1) / a.HG;
   const int64_t per_slot = static_cast<int64_t>(a.HG) * 2 * W;
@@ -490,8 +524,12 @@ int move(const RowsCall& c, const char* name) {
   if (n == 0 || c.H == 0 || c.L == 0) return EVS_OK;
   EVS_REQUIRE(c.layer_ptrs != nullptr && c.heads != nullptr && c.rows != nullptr,
               "%s: null pointer", name);
-  EVS_REQUIRE(I == kByBlocks ? c.blocks != nullptr : c.slots != nullptr, "%s: null index", name);
+  EVS_REQUIRE(I == kByBlocks ? c.blocks != nullptr
+              : I == kByRanges ? c.starts != nullptr && c.first_rows != nullptr
+                               : c.slots != nullptr,
+              "%s: null index", name);
   EVS_REQUIRE(I != kByPairs || c.rows_of != nullptr, "%s: null row list", name);
+  EVS_REQUIRE(I != kByRanges || c.nranges >= 1, "%s: rows to move but no range", name);
 
   const int64_t e = c.elem;
   RowsArgs a{};
@@ -502,6 +540,9 @@ int move(const RowsCall& c, const char* name) {
   a.rows = c.rows;
   a.slots_out = c.slots_out;
   a.rows_of = c.rows_of;
+  a.starts = c.starts;
+  a.first_rows = c.first_rows;
+  a.nranges = c.nranges;
   a.n = n;
   a.cap = c.cap;
   a.half_bytes = c.d * e;
@@ -587,4 +628,19 @@ extern "C" int evs_scatter_pairs(const int64_t* layer_ptrs, int64_t num_layers,
                   const_cast<char*>(static_cast<const char*>(in)), capacity, head_dim,
                   block_size, strides, elem_size, nullptr, rows_of, evs::as_stream(stream)};
   return evs::move<evs::kScatter, evs::kByPairs>(c, "evs_scatter_pairs");
+}
+
+extern "C" int evs_scatter_ranges(const int64_t* layer_ptrs, int64_t num_layers,
+                                  const int64_t* starts, const int64_t* first_rows,
+                                  int64_t num_ranges, int64_t num_rows, const int64_t* heads,
+                                  int64_t num_heads, const void* in, int64_t capacity,
+                                  int64_t head_dim, int64_t block_size, const int64_t* strides,
+                                  int64_t elem_size, void* stream) {
+  evs::clear_error();
+  EVS_REQUIRE(num_ranges >= 0, "evs_scatter_ranges: negative range count");
+  evs::RowsCall c{layer_ptrs, num_layers, nullptr, nullptr, num_rows, heads, num_heads,
+                  const_cast<char*>(static_cast<const char*>(in)), capacity, head_dim,
+                  block_size, strides, elem_size, nullptr, nullptr, evs::as_stream(stream),
+                  starts, first_rows, num_ranges};
+  return evs::move<evs::kScatter, evs::kByRanges>(c, "evs_scatter_ranges");
 }

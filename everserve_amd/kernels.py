@@ -163,6 +163,8 @@ _SIGNATURES: tuple[tuple[str, object, tuple], ...] = (
     ("evs_scatter_rows", _I32, (_P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _P, _I64, _P)),
     ("evs_scatter_pairs", _I32,
      (_P, _I64, _P, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _P, _I64, _P)),
+    ("evs_scatter_ranges", _I32,
+     (_P, _I64, _P, _P, _I64, _I64, _P, _I64, _P, _I64, _I64, _I64, _P, _I64, _P)),
     ("evs_order_pairs_workspace", _I32, (_I64, _I32, _P)),
     ("evs_order_pairs", _I32, (_P, _I64, _I32, _P, _P, _P, _I64, _P)),
     ("evs_order_pairs_static", _I32, (_P, _I64, _I32, _P, _P, _P)),
@@ -406,6 +408,50 @@ class Kernels:
                     lp, layer_ptrs.numel(), sp, rp, slots.numel(), hp, heads.numel(), int(in_ptr),
                     int(capacity), int(d), int(block_size), st, int(elem_size),
                     _stream_of(slots.device),
+                )
+            )
+
+    def scatter_ranges(
+        self,
+        layer_ptrs,
+        starts,
+        first_rows,
+        num_rows: int,
+        heads,
+        in_ptr: int,
+        capacity: int,
+        d: int,
+        block_size: int,
+        strides: Sequence[int],
+        elem_size: int,
+    ) -> None:
+        """Write staged rows [L, H, cap, 2, d] into the caches at the slots of written ranges:
+        row t goes to ``starts[k] + t - first_rows[k]`` for the range k holding it.
+
+        ``starts`` (R) and ``first_rows`` (R + 1: 0 first, ascending, ``num_rows`` last) are int64
+        device tensors. :meth:`scatter_rows` with the slots given as (start, count) ranges;
+        replaces the restore's ``PagedKV.write_rows`` of a table's written ranges
+        (core/everserve/state/mirror.py:926-937).
+        """
+        import torch
+
+        if len(strides) != 5:
+            raise RuntimeError("scatter_ranges: a layout is five strides")
+        if first_rows.numel() != starts.numel() + 1:
+            raise RuntimeError(f"scatter_ranges: {starts.numel()} ranges need "
+                               f"{starts.numel() + 1} first rows, got {first_rows.numel()}")
+        lp = _device_ptr(layer_ptrs, "scatter_ranges: layer_ptrs", torch.long)
+        sp = _device_ptr(starts, "scatter_ranges: starts", torch.long)
+        fp = _device_ptr(first_rows, "scatter_ranges: first_rows", torch.long)
+        hp = _device_ptr(heads, "scatter_ranges: heads", torch.long)
+        _one_device("scatter_ranges", layer_ptrs, starts, first_rows, heads)
+        st = (ctypes.c_int64 * 5)(*[int(s) for s in strides])
+        with torch.cuda.device(starts.device):
+            self._check(
+                self._lib.evs_scatter_ranges(
+                    lp, layer_ptrs.numel(), sp, fp, starts.numel(), int(num_rows), hp,
+                    heads.numel(), int(in_ptr), int(capacity), int(d), int(block_size), st,
+                    int(elem_size), _stream_of(starts.device),
                 )
             )
 

@@ -10,7 +10,7 @@ maps it from shared memory as ``[num_slots, 2, d]``, gathers the written rows on
 row size and slot count), so a bad table refuses the restore before anything is written. It then
 groups the tables of a layer that share their written ranges (a store commit writes every held
 head of a layer at the same slots) and restores each group in chunks, one scatter launch a chunk
-(``evs_scatter_rows`` with the group's head slots, the layer's own strides) writing all of the
+(``evs_scatter_ranges`` with the group's head slots, the layer's own strides) writing all of the
 group's heads: each cache block's rows are covered whole, in increasing slot order. A chunk
 reaches the device in pieces, which keeps three things busy at once: host threads gathering
 piece i+1's rows of all the group's tables side by side into a pinned buffer
@@ -20,9 +20,9 @@ straight into its place in the chunk's ``[tables, rows, 2, d]`` layout, so that 
 small (the pipeline fills and drains sooner) while the scatters are large (a launch's ramp and
 tail weigh less). The copies run on a stream of their own, so the copy engine goes from one piece
 to the next without waiting for a scatter; events order each scatter after its chunk's copies
-and each chunk's copies after the scatter that last read its device buffer. A chunk of one slot
-range gets its slot ids from ``torch.arange`` on the device instead of a copy. Rows land byte for
-byte where ``write_rows`` puts them.
+and each chunk's copies after the scatter that last read its device buffer. The scatter takes the
+chunk's slots as the store's (start, count) ranges (``evs_scatter_ranges``), copied with the
+chunk: no slot ids are built or copied. Rows land byte for byte where ``write_rows`` puts them.
 """
 
 from __future__ import annotations
@@ -173,11 +173,13 @@ class Restorer:
             raise ValueError("scales: a float32 device tensor with one entry per layer")
         nb, rows = self._chunk_bytes, self._chunk_bytes // self._row_bytes
         self._host = [torch.empty(nb, dtype=torch.uint8, pin_memory=True) for _ in range(2)]
-        self._host_slots = [torch.empty(rows, dtype=torch.long, pin_memory=True)
-                            for _ in range(2)]
+        # a chunk's ranges: its starts, then its first rows (one more); a range holds a row or
+        # more, so a chunk of n rows has at most n ranges
+        self._host_ranges = [torch.empty(2 * rows + 1, dtype=torch.long, pin_memory=True)
+                             for _ in range(2)]
         self._dev = [torch.empty(nb, dtype=torch.uint8, device=self.device) for _ in range(2)]
-        self._dev_slots = [torch.empty(rows, dtype=torch.long, device=self.device)
-                           for _ in range(2)]
+        self._dev_ranges = [torch.empty(2 * rows + 1, dtype=torch.long, device=self.device)
+                            for _ in range(2)]
         self._heads: dict[tuple[int, ...], torch.Tensor] = {}
         self._copy_stream = torch.cuda.Stream(device=self.device)
         # per buffer: its last copy to the device (the pinned buffer is free after it) and its last
@@ -235,6 +237,10 @@ class Restorer:
             if ends.max() > geo.num_slots:
                 raise ValueError(f"{name}: a written range ends at slot {int(ends.max())}, past "
                                  f"this cache's {geo.num_slots} slots")
+            live = counts > 0  # an empty range writes nothing
+            starts, counts = starts[live], counts[live]
+            if not len(starts):
+                continue
             key = (layer, starts.tobytes(), counts.tobytes(), rows.nbytes)
             g = groups.get(key)
             if g is None:
@@ -334,23 +340,21 @@ class Restorer:
                     self._ext.copy_rows_async(dev + off, host + off, k, (p1 - p0) * rb, n * rb,
                                               self.device)
             st, ct = self._ranges(g, first_row, c0, c1)
-            one_range = len(st) == 1
+            r = len(st)
+            ranges = self._host_ranges[buf].numpy()
+            ranges[:r] = st
+            ranges[r] = 0
+            np.cumsum(ct, out=ranges[r + 1:2 * r + 1])
             with torch.cuda.stream(self._copy_stream):
-                if not one_range:
-                    slots = self._host_slots[buf].numpy()
-                    at = 0
-                    for s, c in zip(st.tolist(), ct.tolist()):
-                        slots[at:at + c] = np.arange(s, s + c, dtype=np.int64)
-                        at += c
-                    self._dev_slots[buf][:n].copy_(self._host_slots[buf][:n], non_blocking=True)
+                self._ext.copy_rows_async(self._dev_ranges[buf].data_ptr(),
+                                          self._host_ranges[buf].data_ptr(), 1, (2 * r + 1) * 8,
+                                          (2 * r + 1) * 8, self.device)
                 self._copied[buf] = self._copy_stream.record_event()
-            if one_range:
-                torch.arange(int(st[0]), int(st[0]) + n, dtype=torch.long, device=self.device,
-                             out=self._dev_slots[buf][:n])
             stream.wait_event(self._copied[buf])
-            self._ext.scatter_rows(layer_ptr, self._dev_slots[buf][:n], heads, dev, n,
-                                   self.paged.head_dim, self.paged.block_size,
-                                   self._strides[layer], self._elem)
+            dr = self._dev_ranges[buf]
+            self._ext.scatter_ranges(layer_ptr, dr[:r], dr[r:2 * r + 1], n, heads, dev, n,
+                                     self.paged.head_dim, self.paged.block_size,
+                                     self._strides[layer], self._elem)
             self._scattered[buf] = stream.record_event()
             self._launches += 1
             buf ^= 1

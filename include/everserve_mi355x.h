@@ -115,6 +115,22 @@ int evs_scatter_pairs(const int64_t* layer_ptrs, int64_t num_layers, const int64
                       int64_t block_size, const int64_t* strides, int64_t elem_size,
                       void* stream);
 
+/* The scatter of written ranges: staged row t of [num_layers, num_heads, capacity, 2, head_dim]
+ * goes to slot starts[k] + (t - first_rows[k]), for the range k with first_rows[k] <= t <
+ * first_rows[k + 1], t < num_rows, at head slots heads[h]. starts (num_ranges entries) and
+ * first_rows (num_ranges + 1: first_rows[0] = 0, ascending, the last one num_rows) are device
+ * arrays; an empty range is passed over. This is evs_scatter_rows with the slots given as the
+ * store's (start, count) ranges (proto/everserve/proto/mirror.proto:102-117) instead of one id a
+ * row: no slot array to build or copy. With the ranges ascending, as a restore's are
+ * (store/src/storage.rs:430-451), the writes run through each layer's cache front to back and the
+ * launch deals each XCD a contiguous part of them. Replaces the restore's per-table
+ * PagedKV.write_rows of a table's written ranges (core/everserve/state/mirror.py:926-937). */
+int evs_scatter_ranges(const int64_t* layer_ptrs, int64_t num_layers, const int64_t* starts,
+                       const int64_t* first_rows, int64_t num_ranges, int64_t num_rows,
+                       const int64_t* heads, int64_t num_heads, const void* in, int64_t capacity,
+                       int64_t head_dim, int64_t block_size, const int64_t* strides,
+                       int64_t elem_size, void* stream);
+
 /* The pairs for evs_scatter_pairs in slot order, on the device, for a caller whose slot list is
  * in HBM: slots_out[i] = slots[rows_out[i]], by increasing slot, where rows_out is a permutation
  * of 0..num_pairs-1 (stable: equal slots keep their listed order). Only the low key_bits bits of

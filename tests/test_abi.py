@@ -67,6 +67,23 @@ def test_bad_arguments_are_refused_with_a_message(lib):
     assert rc == 1 and b"null" in lib.evs_last_error()
     rc = lib.evs_copy_rows_async(None, None, 2, 16, 8, None)
     assert rc == 1 and b"pitch" in lib.evs_last_error()
+    # the range scatter: a negative range count, rows but no range, more rows than the staging
+    # holds, no range arrays; nothing to move is a success
+    fake = ctypes.c_void_p(1 << 20)  # never dereferenced: each call stops at its checks
+    rc = lib.evs_scatter_ranges(fake, 1, fake, fake, -1, 4, fake, 2, fake, 8, 8, 4, strides, 2,
+                                None)
+    assert rc == 1 and b"negative range" in lib.evs_last_error()
+    rc = lib.evs_scatter_ranges(fake, 1, fake, fake, 0, 4, fake, 2, fake, 8, 8, 4, strides, 2,
+                                None)
+    assert rc == 1 and b"no range" in lib.evs_last_error()
+    rc = lib.evs_scatter_ranges(fake, 1, fake, fake, 1, 9, fake, 2, fake, 8, 8, 4, strides, 2,
+                                None)
+    assert rc == 1 and b"capacity" in lib.evs_last_error()
+    rc = lib.evs_scatter_ranges(fake, 1, None, fake, 1, 4, fake, 2, fake, 8, 8, 4, strides, 2,
+                                None)
+    assert rc == 1 and b"null index" in lib.evs_last_error()
+    assert lib.evs_scatter_ranges(fake, 1, None, None, 0, 0, fake, 2, fake, 8, 8, 4, strides, 2,
+                                  None) == 0
 
 
 def test_the_build_is_stamped_with_this_trees_sources():
@@ -96,6 +113,9 @@ def test_a_launch_past_the_work_item_limit_is_refused_before_launch(lib):
     assert rc == 1 and b"work-items" in lib.evs_last_error()
     rc = lib.evs_scatter_rows(fake, 32, fake, 2 * n, fake, 8, ctypes.c_void_p(1 << 21), 2 * n,
                               128, 16, strides, 2, None)
+    assert rc == 1 and b"work-items" in lib.evs_last_error()
+    rc = lib.evs_scatter_ranges(fake, 32, fake, fake, 1, 2 * n, fake, 8, ctypes.c_void_p(1 << 21),
+                                2 * n, 128, 16, strides, 2, None)
     assert rc == 1 and b"work-items" in lib.evs_last_error()
 
 

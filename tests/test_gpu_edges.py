@@ -310,3 +310,60 @@ def test_scatter_pairs_fp8_and_empty(ext):
     with pytest.raises(RuntimeError, match="slots but"):
         ext.scatter_pairs(ptrs(gpu), dev_long(slots), dev_long(rows_of[:-1]), dev_long([0]),
                           r.data_ptr(), cap, 8, BS, list(strides_of(gpu[0])), 1)
+
+
+def test_scatter_ranges_at_a_restore_chunks_size_equals_the_slot_scatter(ext):
+    """A restore's chunk as the Restorer launches it (one layer, 8 heads, 65,536 rows of a
+    [2, 16384, 16, 8, 128] bf16 cache, 256 MiB): one range, then three (a gap, an empty range,
+    the last slot of the cache reached), each equal to evs_scatter_rows at the same slots."""
+    nb, bs, h, d, n = 16384, 16, 8, 128, 65536
+    g = torch.Generator(device="cuda").manual_seed(31)
+    rows = torch.randn((1, h, n, 2, d), generator=g, device="cuda").to(torch.bfloat16)
+    heads = dev_long([3, 1, 0, 2, 7, 6, 5, 4])
+    for starts, counts in (([100_000], [n]),
+                           ([0, 70_000, nb * bs - 30_000], [35_536, 0, 30_000])):
+        slots = np.concatenate([np.arange(a, a + k, dtype=np.int64) for a, k in zip(starts, counts)])
+        assert len(slots) == n
+        first_rows = np.concatenate(([0], np.cumsum(counts))).astype(np.int64)
+        a = torch.zeros((2, nb, bs, h, d), dtype=torch.bfloat16, device="cuda")
+        b = torch.zeros_like(a)
+        st = list(strides_of(a))
+        ext.scatter_ranges(ptrs([a]), dev_long(starts), dev_long(first_rows), n, heads,
+                           rows.data_ptr(), n, d, bs, st, 2)
+        ext.scatter_rows(ptrs([b]), dev_long(slots), heads, rows.data_ptr(), n, d, bs, st, 2)
+        torch.cuda.synchronize()
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16)), starts
+        # and against the oracle on a sample of rows: the slot scatter is pinned to it elsewhere
+        pick = np.sort(np.random.default_rng(31).choice(n, 64, replace=False))
+        got = a[:, slots[pick] // bs, slots[pick] % bs].cpu()      # [2, 64, h, d]
+        want = rows[0][:, pick].cpu()                              # [h, 64, 2, d] in head order
+        order = heads.cpu().tolist()
+        for i, hs in enumerate(order):
+            assert torch.equal(got[:, :, hs].view(torch.int16),
+                               want[i].permute(1, 0, 2).contiguous().view(torch.int16))
+        del a, b
+
+
+def test_scatter_ranges_over_several_layers_and_nothing_to_move(ext):
+    """Three layers in one launch with ranges that do not ascend; then n = 0 moves nothing."""
+    src = caches("blocks_first", 8, torch.bfloat16, n_layers=3, nb=NB, h=H, seed=33)
+    cap = 40
+    starts, counts = [200, 7, 300], [10, 20, 5]
+    slots = np.concatenate([np.arange(a, a + k) for a, k in zip(starts, counts)])
+    rows = oracle.gather_rows(src, slots, [0, 1, 2], cap, 8, BS, strides_of(src[0]), 2)
+    dst = caches("blocks_first", 8, torch.bfloat16, n_layers=3, nb=NB, h=H, seed=34)
+    want = [t.clone() for t in dst]
+    oracle.scatter_rows(want, slots, [2, 0, 1], rows, cap, 8, BS, strides_of(want[0]), 2)
+    gpu = [t.cuda() for t in dst]
+    r = torch.from_numpy(rows.view(np.int16).copy()).cuda()
+    first_rows = [0, 10, 30, 35]
+    ext.scatter_ranges(ptrs(gpu), dev_long(starts), dev_long(first_rows), 35, dev_long([2, 0, 1]),
+                       r.data_ptr(), cap, 8, BS, list(strides_of(gpu[0])), 2)
+    ext.scatter_ranges(ptrs(gpu), dev_long(starts), dev_long(first_rows), 0, dev_long([2, 0, 1]),
+                       r.data_ptr(), cap, 8, BS, list(strides_of(gpu[0])), 2)
+    torch.cuda.synchronize()
+    for g, w in zip(gpu, want):
+        assert np.array_equal(bits(g), bits(w))
+    with pytest.raises(RuntimeError, match="first rows"):
+        ext.scatter_ranges(ptrs(gpu), dev_long(starts), dev_long(first_rows[:-1]), 35,
+                           dev_long([0]), r.data_ptr(), cap, 8, BS, list(strides_of(gpu[0])), 2)

@@ -1,4 +1,4 @@
-"""The four row kernels against the oracle over seeded random cases, byte for byte, on the GPU.
+"""The row kernels against the oracle over seeded random cases, byte for byte, on the GPU.
 
 The cases are the CPU pins' (tests/cases.py:random_case, pinned in tests/test_oracle_random.py):
 every layout, four element types, head dims on the 16-byte path and off it, block sizes that are
@@ -113,6 +113,53 @@ def test_scatter_pairs(ext, seed):
     rows = torch.from_numpy(staged.view(SIGNED[e])).cuda()
     ext.scatter_pairs(ptrs(gpu), dev_long(c["slots"]), dev_long(rows_of), dev_long(c["heads"]),
                       rows.data_ptr(), c["cap"], c["d"], c["bs"], list(strides_of(gpu[0])), e)
+    torch.cuda.synchronize()
+    for a, b in zip(base_gpu, base_cpu):
+        assert np.array_equal(bits(a), bits(b))
+
+
+def random_ranges(rng, num_slots: int, room: int):
+    """Written ranges as a restore gets them: runs of a random written mask, in slot order or
+    (one case in four) shuffled, with empty ranges among them, at most ``room`` rows in all.
+    Returns (starts, counts)."""
+    written = rng.random(num_slots) < rng.uniform(0.2, 0.9)
+    edges = np.flatnonzero(np.diff(np.concatenate(([0], written.view(np.int8), [0]))))
+    starts, counts = list(edges[0::2]), list(edges[1::2] - edges[0::2])
+    for _ in range(int(rng.integers(0, 3))):  # empty ranges anywhere
+        at = int(rng.integers(0, len(starts) + 1))
+        starts.insert(at, int(rng.integers(0, num_slots)))
+        counts.insert(at, 0)
+    starts, counts = np.array(starts, dtype=np.int64), np.array(counts, dtype=np.int64)
+    if len(starts) and rng.random() < 0.25:
+        order = rng.permutation(len(starts))
+        starts, counts = starts[order], counts[order]
+    keep = np.cumsum(counts) <= room
+    if not keep.all():  # trim to the room: the last kept range may be cut short
+        k = int(np.argmin(keep))
+        counts = counts[:k + 1].copy()
+        counts[k] -= int(counts.sum() - room)
+        starts = starts[:k + 1]
+    if len(starts) == 0:
+        starts, counts = np.array([0], dtype=np.int64), np.array([min(1, room)], dtype=np.int64)
+    return starts, counts
+
+
+@pytest.mark.parametrize("seed", SEEDS)
+def test_scatter_ranges(ext, seed):
+    """The range scatter writes what the slot scatter writes at the ranges' slots, expanded."""
+    c = random_case(seed)
+    cpu, base_cpu, gpu, base_gpu = on_device(c)
+    e = cpu[0].element_size()
+    staged = staged_bits(c, len(cpu), e)
+    starts, counts = random_ranges(c["rng"], c["nb"] * c["bs"], c["cap"])
+    slots = np.concatenate([np.arange(a, a + k, dtype=np.int64) for a, k in zip(starts, counts)])
+    first_rows = np.concatenate(([0], np.cumsum(counts))).astype(np.int64)
+    oracle.scatter_rows(cpu, slots, c["heads"], staged, c["cap"], c["d"], c["bs"],
+                        strides_of(cpu[0]), e)
+    rows = torch.from_numpy(staged.view(SIGNED[e])).cuda()
+    ext.scatter_ranges(ptrs(gpu), dev_long(starts), dev_long(first_rows), len(slots),
+                       dev_long(c["heads"]), rows.data_ptr(), c["cap"], c["d"], c["bs"],
+                       list(strides_of(gpu[0])), e)
     torch.cuda.synchronize()
     for a, b in zip(base_gpu, base_cpu):
         assert np.array_equal(bits(a), bits(b))

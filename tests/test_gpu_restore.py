@@ -167,6 +167,25 @@ def test_a_chunk_smaller_than_a_row_of_every_table_still_holds_one(ext, chunk_by
     assert np.array_equal(got, want)
 
 
+def test_empty_written_ranges_are_passed_over(ext):
+    """A table's list of written ranges may hold empty ones: they write nothing and the rest
+    lands; a table whose ranges are all empty is skipped, as one with none is."""
+    nb, bs, h, d = 8, 4, 2, 8
+    src = caches("kv_first", d, torch.bfloat16, n_layers=1, nb=nb, bs=bs, h=h, seed=85)
+    slots = [0, 1, 2, 9, 10]
+    tables, written = commit(src, slots, [0, 1], cap=8)
+    dst = [torch.zeros_like(t).cuda() for t in src]
+    with_empty = [(0, 3), (5, 0), (9, 2), (20, 0)]
+    rows = Restorer(ext, dst).restore([Table(0, tables[0], with_empty),
+                                       Table(1, tables[1], [(4, 0)])], {0: 1, 1: 0})
+    assert rows == len(slots)
+    cpu = dst[0].cpu()
+    got = oracle.gather_rows([cpu], slots, [1], 8, d, bs, strides_of(cpu), 2)
+    want = oracle.gather_rows([src[0]], slots, [0], 8, d, bs, strides_of(src[0]), 2)
+    assert np.array_equal(got, want)
+    assert not cpu[:, :, :, 0].any()  # head slot 0 (table 1's) stays untouched
+
+
 def test_tables_that_do_not_fit_this_ranks_cache_are_refused_before_anything_is_written(ext):
     """A table of a layer this rank lacks, a head slot past the layer's heads, a written range
     past the cache's slots (a table of a larger cache), rows of another size, or two tables into
