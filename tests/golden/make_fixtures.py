@@ -10,8 +10,9 @@ and of the HIP path is checked against the same bytes:
   blocks of 4 slots, 3 head slots and 3 layers; slots [5, -1, 17, 0, 27], held heads [0, 2],
   capacity 8. It covers the 3 layouts x d in {8, 6} x {bf16, f16, f32, fp8 e4m3}. Each case holds
   the caches' raw bits and the rows. For bf16, the caches that a scatter of those rows writes
-  into zeroed caches are also included, and those that the pair scatter writes for the pairs
-  PAIR_SLOTS / PAIR_ROWS below.
+  into zeroed caches are also included, those that the pair scatter writes for the pairs
+  PAIR_SLOTS / PAIR_ROWS below, and those that the range scatter writes for the written ranges
+  RANGE_STARTS / RANGE_COUNTS (the slot scatter at the ranges' slots).
 * reduce_sizes.npz: the ordered sum of core/tests/test_slot_kernel.py:40-55. Members 0..2 at
   sizes {16384, 3000, 2} come from torch.Generator().manual_seed(1000 * rank + n), summed in
   orders [0, 1, 2] and [2, 0, 1]. It also holds the order-sensitive case (big * 2^20,
@@ -45,6 +46,15 @@ BITS = {1: (torch.uint8, np.uint8), 2: (torch.int16, np.uint16), 4: (torch.int32
 # row outside the capacity and one row written to two slots
 PAIR_SLOTS = [27, 3, -1, 9, 5, 20]
 PAIR_ROWS = [0, 4, 2, 9, 1, 4]
+# the range scatter's case: written (start, count) ranges over the literal rows, not in slot order
+# and with an empty one, 8 rows in all (the capacity)
+RANGE_STARTS = [24, 2, 9, 0]
+RANGE_COUNTS = [3, 0, 4, 1]
+
+
+def range_slots() -> np.ndarray:
+    return np.concatenate([np.arange(a, a + k, dtype=np.int64)
+                           for a, k in zip(RANGE_STARTS, RANGE_COUNTS)])
 
 
 def raw(t: torch.Tensor) -> np.ndarray:
@@ -56,6 +66,8 @@ def gather_literal() -> dict[str, np.ndarray]:
     out: dict[str, np.ndarray] = {
         "pair_slots": np.array(PAIR_SLOTS, dtype=np.int64),
         "pair_rows_of": np.array(PAIR_ROWS, dtype=np.int64),
+        "range_starts": np.array(RANGE_STARTS, dtype=np.int64),
+        "range_counts": np.array(RANGE_COUNTS, dtype=np.int64),
         "slots": np.array(SLOTS, dtype=np.int64),
         "heads": np.array(HEADS, dtype=np.int64),
         "capacity": np.array(CAPACITY, dtype=np.int64),
@@ -80,6 +92,10 @@ def gather_literal() -> dict[str, np.ndarray]:
                     oracle.scatter_pairs(zero, PAIR_SLOTS, PAIR_ROWS, HEADS, rows, CAPACITY, d,
                                          BS, strides_of(zero[0]), e)
                     out[f"{key}_paired"] = np.stack([raw(t) for t in zero])
+                    zero = [torch.zeros_like(t) for t in layers]
+                    oracle.scatter_rows(zero, range_slots(), HEADS, rows, CAPACITY, d, BS,
+                                        strides_of(zero[0]), e)
+                    out[f"{key}_ranged"] = np.stack([raw(t) for t in zero])
     return out
 
 

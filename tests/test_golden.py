@@ -21,7 +21,7 @@ import pytest
 import torch
 
 import oracle
-from tests.cases import strides_of
+from tests.cases import brute_scatter, strides_of
 from tests.golden import make_fixtures as mf
 
 GOLDEN = Path(__file__).resolve().parent / "golden"
@@ -77,6 +77,27 @@ def test_the_oracle_scatters_the_stored_pairs(case):
                          G[f"{case}_rows"], int(G["capacity"]), d, int(G["block_size"]),
                          strides_of(layers[0]), 2)
     assert np.array_equal(np.stack([mf.raw(t) for t in layers]), G[f"{case}_paired"])
+
+
+def stored_range_slots() -> np.ndarray:
+    return np.concatenate([np.arange(a, a + k, dtype=np.int64)
+                           for a, k in zip(G["range_starts"], G["range_counts"])])
+
+
+@pytest.mark.parametrize("case", [c for c in CASES if c.endswith("bf16")])
+def test_the_stored_range_scatter_is_the_scatter_at_the_ranges_slots(case):
+    """The range case's caches: the oracle's slot scatter at the ranges' slots writes them, and
+    so does the scatter by its definition per layout (tests/cases.py:brute_scatter)."""
+    slots = stored_range_slots()
+    assert len(slots) == int(G["capacity"])
+    layers = [torch.zeros_like(t) for t in tensors(case)]
+    d = int(case.rsplit("_", 2)[1][1:])
+    rows = G[f"{case}_rows"]
+    brute = np.stack(brute_scatter(layers, slots, G["heads"], rows))
+    oracle.scatter_rows(layers, slots, G["heads"], rows, int(G["capacity"]), d,
+                        int(G["block_size"]), strides_of(layers[0]), 2)
+    assert np.array_equal(np.stack([mf.raw(t) for t in layers]), G[f"{case}_ranged"])
+    assert np.array_equal(brute.view(np.uint16), G[f"{case}_ranged"])
 
 
 def test_the_stored_inputs_still_come_from_the_seeds():

@@ -2,7 +2,7 @@
 
 The fixtures hold the inputs and the expected bytes (tests/golden/make_fixtures.py):
 * the gather and the scatter of the reference tests' literal case, in every layout, d in {8, 6},
-  and bf16, f16, f32 and fp8, and the pair scatter of its rows;
+  and bf16, f16, f32 and fp8, and the pair and range scatters of its rows;
 * the ordered sums at the reference's sizes {16384, 3000, 2}, and the order-sensitive case, through
   evs_local_reduce;
 * config C1 (Qwen2.5-0.5B shape), whose rows are checked against their
@@ -68,6 +68,22 @@ def test_the_pair_scatter_writes_the_stored_caches(ext, case):
     torch.cuda.synchronize()
     got = np.stack([mf.raw(t.cpu()) for t in layers])
     assert np.array_equal(got, G[f"{case}_paired"])
+
+
+@pytest.mark.parametrize("case", [c for c in CASES if c.endswith("bf16")])
+def test_the_range_scatter_writes_the_stored_caches(ext, case):
+    layers = [torch.zeros_like(t).cuda() for t in tensors(case)]
+    rows = torch.from_numpy(G[f"{case}_rows"].view(np.int16).copy()).cuda()
+    d = int(case.rsplit("_", 2)[1][1:])
+    counts = G["range_counts"]
+    first_rows = np.concatenate(([0], np.cumsum(counts)))
+    ext.scatter_ranges(dev_long([t.data_ptr() for t in layers]), dev_long(G["range_starts"]),
+                       dev_long(first_rows), int(first_rows[-1]), dev_long(G["heads"]),
+                       rows.data_ptr(), int(G["capacity"]), d, int(G["block_size"]),
+                       list(strides_of(layers[0])), 2)
+    torch.cuda.synchronize()
+    got = np.stack([mf.raw(t.cpu()) for t in layers])
+    assert np.array_equal(got, G[f"{case}_ranged"])
 
 
 def reduce(ext, members, order):
