@@ -16,10 +16,10 @@
 // row after row), so a wave stores whole rows: 1 KiB contiguous for bf16 d=128. For the gather
 // the tile numbers run through a slot range's head groups first, so the workgroups reading the
 // heads of one cache block (adjacent in every paged layout) are neighbours, dealt round-robin to
-// the XCDs; the slot scatter's XCD remap (xcd_tile) keeps runs of 64 neighbouring tiles on one
-// XCD, and the range scatter gives each XCD one contiguous part of the grid. Tiles are kept
-// small (a few KiB) and numerous: on MI355X many short
-// independent workgroups keep more bytes in flight than fewer long ones. Measured and rejected:
+// the XCDs; the slot and pair scatters' XCD remap (xcd_tile) keeps runs of 64 neighbouring tiles
+// on one XCD, and the range scatter's gives each XCD one contiguous part of the grid. Tiles are
+// kept small (a few KiB) and numerous: on MI355X many short independent workgroups keep more
+// bytes in flight than fewer long ones. Measured and rejected:
 // a persistent grid with prefetched indices, and an LDS-staged transpose that reads a tile in
 // cache order and writes it in staging order (both slower on every config); for the scatter,
 // words in cache order and issuing a tile's loads before its slot ids are read (both slower);
@@ -77,6 +77,16 @@ namespace {
 #ifndef EVS_SCATTER_XCD_CHUNK
 #define EVS_SCATTER_XCD_CHUNK 64
 #endif
+// The scatter of written ranges (staged rows to the slots of (start, count) ranges, which ascend
+// in a restore) gives each XCD one contiguous part of the grid, so that the XCDs write the cache
+// in 8 streams that each run front to back. On ascending slots that measured faster than runs of
+// 64 on every box tried: a restore's chunk (1 layer, 8 heads, 65,536 slots) 6,339 against 5,735
+// GB/s for an isolated launch; 16 layers of C4's cache 5,801-6,144 against 5,447-5,537. For the
+// slot scatter's permuted slots it depended on the box (16 layers: 4.8 % faster on two runs, 2.4 %
+// slower on another; C4's 32 layers 2 % slower), so that one keeps runs of 64.
+#ifndef EVS_RANGES_XCD_CHUNK
+#define EVS_RANGES_XCD_CHUNK -1
+#endif
 constexpr uint32_t kXcds = 8;
 // The pair scatter (a staged row per listed slot, listed in the order the caller wants written):
 // its tiles span all heads (2 slots x 8 heads at bf16 d=128, 8 KiB) and its words run along the
@@ -104,14 +114,6 @@ constexpr uint32_t kXcds = 8;
 #endif
 #ifndef EVS_PAIRS_VPT
 #define EVS_PAIRS_VPT 2
-#endif
-// The scatter of written ranges (staged rows to the slots of (start, count) ranges, which ascend
-// in a restore): each XCD takes one contiguous part of the grid (chunk -1), so that the XCDs write
-// the cache in 8 streams that each run front to back. On a restore's chunk (1 layer, 8 heads,
-// 65,536 ascending slots, 256 MiB of rows) that measured 6,339 GB/s against 5,735 for the slot
-// scatter's chunk of 64, isolated launches.
-#ifndef EVS_RANGES_XCD_CHUNK
-#define EVS_RANGES_XCD_CHUNK -1
 #endif
 // Tile shape per direction: words a tile aims at, heads it covers (0: all), head groups fastest.
 #ifndef EVS_GATHER_TILE_WORDS
