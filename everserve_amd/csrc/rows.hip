@@ -177,7 +177,11 @@ static_assert(threads_of(kGather, kBySlots) * vpt_of(kGather, kBySlots) <= kSink
 // every memory operation in flight before each store, which serialises a thread's stores (the
 // gather measured 1 % faster without). The scatter keeps the branches: its scattered stores ran
 // 0.5-1.5 % faster serialised than all in flight. The contents are never read as data.
-__device__ u32x4 g_sink[kSinkWords];
+// Workgroups take one of kSinkCopies regions by id: with one region shared by all, a call whose
+// tiles leave most lanes idle (a decode step of 1-4 slots) sent every such store to the same
+// 16 KiB, and so to the same few memory channels, and took 4.5 us where 8 slots took 2.45.
+constexpr int kSinkCopies = 64;
+__device__ u32x4 g_sink[kSinkCopies * kSinkWords];
 
 struct RowsArgs {
   const int64_t* layer_ptrs;  // device: each layer's cache base address
@@ -369,7 +373,8 @@ __device__ __forceinline__ void move_tile(const RowsArgs& a, const int64_t* s_sl
   char* rows_l = a.rows + static_cast<int64_t>(layer) * a.H * a.cap * (2 * a.half_bytes);
 
   constexpr int kThreads = threads_of(D, I);
-  char* sink = reinterpret_cast<char*>(g_sink) + tid * sizeof(u32x4);
+  char* sink = reinterpret_cast<char*>(g_sink + (blockIdx.x % kSinkCopies) * kSinkWords) +
+               tid * sizeof(u32x4);
   constexpr int kVpt = vpt_of(D, I);
   for (uint32_t v0 = 0; v0 < a.tile_words; v0 += kThreads * kVpt) {
     T w[kVpt];
