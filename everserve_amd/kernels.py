@@ -50,6 +50,31 @@ REDUCE_STATE_WORDS = 288
 """64-bit words of local_reduce's state record (EVS_REDUCE_STATE_WORDS in the C header)."""
 
 
+class BoundGather:
+    """``evs_gather_rows`` for fixed layers, heads and layout (:meth:`Kernels.bind_gather`)."""
+
+    def __init__(self, kernels: "Kernels", lp: int, num_layers: int, hp: int, num_heads: int,
+                 d: int, block_size: int, strides: list[int], elem_size: int, device: int,
+                 keep: tuple) -> None:
+        self._kernels = kernels
+        self._fn = kernels._lib.evs_gather_rows
+        self._args = (lp, num_layers, hp, num_heads, d, block_size)
+        self._strides = (ctypes.c_int64 * 5)(*strides)
+        self._elem = elem_size
+        self.device = device
+        self._keep = keep  # the tensors whose addresses the launcher holds
+
+    def __call__(self, slots_ptr: int, n: int, out_ptr: int, capacity: int, stream: int) -> None:
+        """Enqueue the gather of rows ``[0, n)`` at ``slots_ptr`` (int64 device slot ids) into
+        ``[L, H, capacity, 2, d]`` at ``out_ptr`` on ``stream`` (a raw stream handle of the
+        bound device, which must be the current device)."""
+        lp, num_layers, hp, num_heads, d, bs = self._args
+        rc = self._fn(lp, num_layers, slots_ptr, n, hp, num_heads, out_ptr, capacity, d, bs,
+                      self._strides, self._elem, stream)
+        if rc != EVS_OK:
+            self._kernels._check(rc)
+
+
 @dataclass(frozen=True)
 class CommitPlan:
     """``evs_store_commit``'s per-table arguments for one set of store tables, built once."""
@@ -294,6 +319,23 @@ class Kernels:
                     _stream_of(slots.device),
                 )
             )
+
+    def bind_gather(self, layer_ptrs, heads, d: int, block_size: int, strides: Sequence[int],
+                    elem_size: int) -> "BoundGather":
+        """:meth:`gather_rows` with the arguments that stay the same from step to step (the
+        layers, the held heads, the layout) checked and converted once; the returned launcher
+        takes a step's slot ids, row count, output and stream. For a step path that launches
+        every step, where the checks and conversions cost more host time than the launch."""
+        import torch
+
+        if len(strides) != 5:
+            raise RuntimeError("gather_rows: a layout is five strides")
+        lp = _device_ptr(layer_ptrs, "gather_rows: layer_ptrs", torch.long)
+        hp = _device_ptr(heads, "gather_rows: heads", torch.long)
+        _one_device("gather_rows", layer_ptrs, heads)
+        return BoundGather(self, lp, layer_ptrs.numel(), hp, heads.numel(), int(d),
+                           int(block_size), [int(s) for s in strides], int(elem_size),
+                           layer_ptrs.device.index, (layer_ptrs, heads))
 
     def gather_blocks(
         self,

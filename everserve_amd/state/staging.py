@@ -291,6 +291,7 @@ class StepStager:
         ordered = sorted((layer_index(n), n, t) for n, t in kv_caches.items())
         self.layers = [(n, t) for _, n, t in ordered]
         self._layer_of = {n: i for i, (n, _) in enumerate(self.layers)}
+        self._layer_ptr = [t.data_ptr() for _, t in self.layers]
         first = self.layers[0][1]
         if not first.is_cuda:
             raise ValueError("the step path stages device caches")
@@ -303,6 +304,12 @@ class StepStager:
         self._ext = ext
         self._kernel = GatherKernel(ext, [t for _, t in self.layers], self.paged)
         self._heads_dev = torch.tensor(self.heads, dtype=torch.long, device=self.device)
+        # a step of every layer is one launch whose fixed arguments are checked once, here
+        self._launch = None
+        if self._kernel.uniform:
+            self._launch = ext.bind_gather(self._kernel._ptrs, self._heads_dev,
+                                           self.paged.head_dim, self.paged.block_size,
+                                           self._kernel._strides[0], self._kernel.elem)
         if scales is not None and (not scales.is_cuda or scales.device != self.device
                                    or scales.dtype != torch.float32
                                    or scales.shape[0] != len(self.layers)):
@@ -352,7 +359,7 @@ class StepStager:
         """
         self._check_failed()
         layer = self._layer_of[layer_name]
-        if self.layers[layer][1].data_ptr() != kv_layer.data_ptr():
+        if self._layer_ptr[layer] != kv_layer.data_ptr():
             raise ValueError(f"layer {layer_name} is not the cache tensor the stager was given")
         g = self._step
         if g is None:
@@ -366,8 +373,14 @@ class StepStager:
         n = int(slots.shape[0])
         stage = self._staging(n)
         # the step's own copy of its slot ids, ordered on the producing stream, so a later
-        # change to the caller's tensor cannot reach the gather or the descriptor
-        stage.device_slots[:n].copy_(slots.reshape(-1), non_blocking=True)
+        # change to the caller's tensor cannot reach the gather or the descriptor; int64 ids on
+        # this device (a serving engine's slot mapping) take one copy call, anything else torch's
+        if (slots.device == self.device and slots.dtype == torch.long
+                and slots.is_contiguous()):
+            self._ext.copy_rows_async(stage.device_slots.data_ptr(), slots.data_ptr(), 1, n * 8,
+                                      n * 8, self.device)
+        else:
+            stage.device_slots[:n].copy_(slots.reshape(-1), non_blocking=True)
         return StepGather(n, self.heads, stage)
 
     def commit(self, epoch: int, step: int, committed_tokens: Mapping) -> None:
@@ -380,9 +393,14 @@ class StepStager:
         job.times["commit"] = t0
         if g is not None and g.filled:
             cur = torch.cuda.current_stream(self.device)
-            self._kernel.gather(g.stage.device_slots[:g.n], self._heads_dev,
-                                g.stage.device_rows.data_ptr(), g.stage.capacity,
-                                sorted(g.filled))
+            if (self._launch is not None and len(g.filled) == len(self.layers)
+                    and torch.cuda.current_device() == self._launch.device):
+                self._launch(g.stage.device_slots.data_ptr(), g.n, g.stage.device_rows.data_ptr(),
+                             g.stage.capacity, cur.cuda_stream)
+            else:
+                self._kernel.gather(g.stage.device_slots[:g.n], self._heads_dev,
+                                    g.stage.device_rows.data_ptr(), g.stage.capacity,
+                                    sorted(g.filled))
             self._snapshot_scales(g.stage)
             job.gathered = self._event()
             self._ext.event_record(job.gathered, cur)
