@@ -367,3 +367,28 @@ def test_scatter_ranges_over_several_layers_and_nothing_to_move(ext):
     with pytest.raises(RuntimeError, match="first rows"):
         ext.scatter_ranges(ptrs(gpu), dev_long(starts), dev_long(first_rows[:-1]), 35,
                            dev_long([0]), r.data_ptr(), cap, 8, BS, list(strides_of(gpu[0])), 2)
+
+
+@pytest.mark.parametrize("layout", LAYOUTS)
+def test_a_bound_gather_writes_what_gather_rows_writes(ext, layout):
+    """Kernels.bind_gather (the step path's launcher, its fixed arguments checked once) against
+    gather_rows on the same caches, slots (padding included) and held heads; a layout of four
+    strides is refused when binding."""
+    src = [t.cuda() for t in caches(layout, 8, torch.bfloat16, n_layers=L, nb=NB, h=H, seed=41)]
+    slots = dev_long([5, -1, 17, 0, 27, 300, 31])
+    heads = dev_long([2, 0])
+    st = list(strides_of(src[0]))
+    cap = 8
+    a = torch.full((L, 2, cap, 2, 8), 7, dtype=torch.bfloat16, device="cuda")
+    b = torch.full_like(a, 7)
+    ext.gather_rows(ptrs(src), slots, heads, a.data_ptr(), cap, 8, BS, st, 2)
+    launch = ext.bind_gather(ptrs(src), heads, 8, BS, st, 2)
+    launch(slots.data_ptr(), slots.numel(), b.data_ptr(), cap,
+           torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    with pytest.raises(RuntimeError, match="five strides"):
+        ext.bind_gather(ptrs(src), heads, 8, BS, st[:4], 2)
+    with pytest.raises(KernelError, match="capacity"):
+        launch(slots.data_ptr(), slots.numel(), b.data_ptr(), 4,
+               torch.cuda.current_stream().cuda_stream)
