@@ -187,6 +187,7 @@ class Restorer:
         self._copied: list[torch.cuda.Event | None] = [None, None]
         self._scattered: list[torch.cuda.Event | None] = [None, None]
         self.timing: dict[str, float] = {}
+        self._lock = threading.Lock()  # one restore at a time owns the buffers and events
 
     def _head_list(self, heads: Sequence[int]) -> torch.Tensor:
         key = tuple(heads)
@@ -256,8 +257,14 @@ class Restorer:
 
         Every table is checked first (:meth:`plan`); a refused restore writes nothing. Returns the
         rows written, over every table. Synchronises the device at the end, as the reference's
-        restore does (core/everserve/state/mirror.py:938-939).
+        restore does (core/everserve/state/mirror.py:938-939). Restores through one Restorer from
+        several threads run one after another: they share its buffers.
         """
+        with self._lock:
+            return self._restore(tables, head_map, scales)
+
+    def _restore(self, tables: Iterable[Table], head_map: Mapping[int, int],
+                 scales: Mapping[int, Sequence[float]] | None) -> int:
         t0 = time.perf_counter()
         groups = self.plan(tables, head_map)
         side = None

@@ -167,6 +167,44 @@ def test_a_chunk_smaller_than_a_row_of_every_table_still_holds_one(ext, chunk_by
     assert np.array_equal(got, want)
 
 
+def test_two_threads_restoring_through_one_restorer(ext):
+    """Two threads restore through one Restorer at once (different tables, different head slots,
+    small chunks so each restore runs many): the restores take turns on its buffers, and both
+    land."""
+    import threading
+
+    nb, bs, h, d = 64, 4, 4, 16
+    src = caches("kv_first", d, torch.bfloat16, n_layers=2, nb=nb, bs=bs, h=h, seed=87)
+    slots = list(range(0, 200, 3))
+    tables, written = commit(src, slots, [0, 1, 2, 3], cap=128)
+    dst = [torch.zeros_like(t).cuda() for t in src]
+    r = Restorer(ext, dst, chunk_bytes=4 * 8 * 2 * d * 2, piece_bytes=2 * 8 * 2 * d * 2)
+    mine = {0: [t for t in tables if t % 1000 in (0, 1)], 1: [t for t in tables if t % 1000 in (2, 3)]}
+    moves = {0: 3, 1: 2, 2: 1, 3: 0}
+    errors = []
+
+    def run(k):
+        try:
+            for _ in range(3):
+                r.restore([Table(t, tables[t], oracle.written_ranges(written[t])) for t in mine[k]],
+                          moves)
+        except Exception as e:  # noqa: BLE001 - reported below
+            errors.append(e)
+
+    threads = [threading.Thread(target=run, args=(k,)) for k in (0, 1)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors
+    for li in range(2):
+        cpu = dst[li].cpu()
+        got = oracle.gather_rows([cpu], slots, [3, 2, 1, 0], 128, d, bs, strides_of(cpu), 2)
+        want = oracle.gather_rows([src[li]], slots, [0, 1, 2, 3], 128, d, bs,
+                                  strides_of(src[li]), 2)
+        assert np.array_equal(got, want), li
+
+
 def test_empty_written_ranges_are_passed_over(ext):
     """A table's list of written ranges may hold empty ones: they write nothing and the rest
     lands; a table whose ranges are all empty is skipped, as one with none is."""
