@@ -25,6 +25,7 @@ memory.
 from __future__ import annotations
 
 import os
+import threading
 from dataclasses import dataclass, field
 from pathlib import Path
 from typing import Mapping
@@ -101,6 +102,10 @@ class StoreTables:
         self._plans: dict[tuple, object] = {}
         """Per table set a descriptor names, the commit's arguments built once (tables are
         never replaced once created)."""
+        self._lock = threading.RLock()
+        """Commits (the stager's copy thread) and reads (a restore, another thread) take turns
+        on the table set; the rows a restore reads are the store's to keep still, as they are
+        for the Rust store (no commit reaches a lost rank's tables)."""
 
     def _create(self, table: int, row_bytes: int) -> StoreTable:
         nbytes = self.num_slots * row_bytes
@@ -122,6 +127,10 @@ class StoreTables:
         ``stage`` is the staged bytes (uint8), ``step`` the ``StagedStep`` descriptor. Every slot
         id and table must fit before anything is written, as the store checks a descriptor first.
         """
+        with self._lock:
+            return self._commit(stage, step, step_no)
+
+    def _commit(self, stage: np.ndarray, step: Mapping, step_no: int) -> int:
         stage = np.ascontiguousarray(stage).view(np.uint8).reshape(-1)
         rb = row_bytes_of(step)
         key = (tuple(step["layers"]), tuple(step["heads"]), int(step["table_stride"]),
@@ -148,7 +157,8 @@ class StoreTables:
 
     def written_ranges(self, table: int, since_step: int = 0) -> list[tuple[int, int]]:
         """(start, count) runs of the slots written after ``since_step`` (storage.rs:430-451)."""
-        hit = self.tables[table].written_step > since_step
+        with self._lock:
+            hit = self.tables[table].written_step > since_step
         if not hit.any():
             return []
         edges = np.flatnonzero(np.diff(np.concatenate(([0], hit.view(np.int8), [0]))))
@@ -157,10 +167,11 @@ class StoreTables:
     def restore_tables(self, since_step: int = 0) -> list[Table]:
         """Every table that holds rows written after ``since_step``, as a restore reads them."""
         out = []
-        for tid in sorted(self.tables):
-            ranges = self.written_ranges(tid, since_step)
-            if ranges:
-                out.append(Table(tid, self.tables[tid].rows, ranges))
+        with self._lock:
+            for tid in sorted(self.tables):
+                ranges = self.written_ranges(tid, since_step)
+                if ranges:
+                    out.append(Table(tid, self.tables[tid].rows, ranges))
         return out
 
     def crc(self, table: int, slot: int) -> int:
@@ -169,19 +180,22 @@ class StoreTables:
 
     def flush(self) -> None:
         """Write file-backed tables through to their files."""
-        for t in self.tables.values():
-            if isinstance(t.rows, np.memmap):
-                t.rows.flush()
+        with self._lock:
+            for t in self.tables.values():
+                if isinstance(t.rows, np.memmap):
+                    t.rows.flush()
 
     def restore_scales(self) -> dict[int, np.ndarray]:
         """Layer -> its scales as last committed; empty when no step carried any."""
-        if self.scales is None:
-            return {}
-        return {layer: v.copy() for layer, v in enumerate(self.scales)}
+        with self._lock:
+            if self.scales is None:
+                return {}
+            return {layer: v.copy() for layer, v in enumerate(self.scales)}
 
     def sink(self, job) -> None:
         """A :class:`everserve_amd.state.staging.StepStager` sink: commit each staged step."""
         if job.descriptor is not None:
             self.commit(job.stage_bytes, job.descriptor, job.step)
         if getattr(job, "scales", None) is not None:
-            self.scales = np.array(job.scales, dtype=np.float32, copy=True)
+            with self._lock:
+                self.scales = np.array(job.scales, dtype=np.float32, copy=True)

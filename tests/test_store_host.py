@@ -158,6 +158,53 @@ def test_store_tables_reuse_a_table_sets_commit_arguments(ext):
     assert len(store._plans) == 2
 
 
+def test_store_tables_commits_from_two_threads_and_a_reader(ext):
+    """Two threads commit steps of different layers while a third reads the table set as a
+    restore does: the commits take turns, no read sees the set change under it, and every table
+    ends equal to the oracle's."""
+    import threading
+
+    num_slots, d = 256, 8
+    store = StoreTables(ext, num_slots, threads=4)
+    steps = {k: [staged([k], [0, 1], 16, d, 2, list(range(i * 8 + k, i * 8 + k + 8)), seed=i + 50)
+                 for i in range(12)] for k in (0, 1)}
+    errors, done = [], threading.Event()
+
+    def commit(k):
+        try:
+            for i, (stage, desc) in enumerate(steps[k]):
+                store.commit(stage, desc, i + 1)
+        except Exception as e:  # noqa: BLE001 - reported below
+            errors.append(e)
+
+    def read():
+        try:
+            while not done.is_set():
+                for t in store.restore_tables():
+                    assert t.written and t.rows.size == num_slots * 2 * d * 2
+        except Exception as e:  # noqa: BLE001 - reported below
+            errors.append(e)
+
+    reader = threading.Thread(target=read)
+    reader.start()
+    writers = [threading.Thread(target=commit, args=(k,)) for k in (0, 1)]
+    for t in writers:
+        t.start()
+    for t in writers:
+        t.join()
+    done.set()
+    reader.join()
+    assert not errors, errors
+    tables, written, crcs = {}, {}, {}
+    for k in (0, 1):
+        for i, (stage, desc) in enumerate(steps[k]):
+            oracle.store_commit(stage, desc, tables, num_slots, written, i + 1, crcs)
+    assert sorted(store.tables) == sorted(tables)
+    for t, want in tables.items():
+        assert np.array_equal(np.asarray(store.tables[t].rows), want), t
+        assert np.array_equal(store.tables[t].crc, crcs[t]), t
+
+
 def test_a_bad_step_is_refused_before_anything_is_written(ext):
     num_slots, d = 32, 8
     stage, desc = staged([0], [0, 1], 8, d, 2, [3, 4, 40], seed=1)
