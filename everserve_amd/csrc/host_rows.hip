@@ -180,6 +180,40 @@ struct Batch {
   int64_t run0, nruns, offset, len;
 };
 
+// The host copy of the last batch overlaps no copy engine work: it is the delivery's tail. Split
+// the last batch into pieces of 1/2, 1/4, 1/8 and 1/8 of it, by runs when it has 8 or more, else by
+// bytes within its runs (64-byte multiples), so that all but the last piece overlap a copy. Too
+// small a batch is left whole.
+constexpr int64_t kMinSplitBytes = int64_t{1} << 20;
+
+void split_last(std::vector<Batch>& batches) {
+  if (batches.empty()) return;
+  const Batch b = batches.back();
+  if (b.nruns * b.len < kMinSplitBytes) return;
+  std::vector<Batch> pieces;
+  if (b.nruns >= 8) {
+    int64_t r = b.run0;
+    const int64_t end = b.run0 + b.nruns;
+    for (int64_t part : {b.nruns / 2, b.nruns / 4, b.nruns / 8}) {
+      pieces.push_back({r, part, b.offset, b.len});
+      r += part;
+    }
+    pieces.push_back({r, end - r, b.offset, b.len});
+  } else {
+    if (b.len < 8 * 64) return;
+    int64_t o = b.offset;
+    const int64_t end = b.offset + b.len;
+    for (int64_t div : {2, 4, 8}) {
+      const int64_t part = (b.len / div) & ~int64_t{63};
+      pieces.push_back({b.run0, b.nruns, o, part});
+      o += part;
+    }
+    pieces.push_back({b.run0, b.nruns, o, end - o});
+  }
+  batches.pop_back();
+  batches.insert(batches.end(), pieces.begin(), pieces.end());
+}
+
 int deliver(char* dst, int64_t dst_pitch, const char* src, int64_t src_pitch, int64_t runs,
             int64_t run_bytes, char* const bounce[2], int64_t bounce_bytes, int64_t max_threads,
             hipStream_t stream, hipEvent_t ev[2]) {
@@ -192,6 +226,7 @@ int deliver(char* dst, int64_t dst_pitch, const char* src, int64_t src_pitch, in
       for (int64_t o = 0; o < run_bytes; o += bounce_bytes)
         batches.push_back({r, 1, o, std::min(bounce_bytes, run_bytes - o)});
   }
+  split_last(batches);
   auto issue = [&](size_t i) -> int {
     const Batch& b = batches[i];
     // one run has no pitch of its own: give the copy its width (the caller's may be smaller)

@@ -37,6 +37,11 @@ pytestmark = pytest.mark.gpu
     (256, 32768, 65536, 32 << 20),  # a decode step's shape: one batch
     (3, 64, 128, 64),               # a run exactly a bounce buffer
     (1, 4096, 64, 1024),            # one run: its pitch, smaller than the run, is not used
+    # the last batch split into 1/2, 1/4, 1/8, 1/8: by bytes within 3 runs of an odd length,
+    # by bytes after two full batches, and by runs
+    (3, (3 << 20) + 100, (3 << 20) + 128, 16 << 20),
+    (10, 2 << 20, 2 << 20, 8 << 20),
+    (20, 300000, 300032, 8 << 20),
 ])
 def test_deliver_rows_into_memory_that_is_not_pinned(ext, runs, run_bytes, pitch, bounce):
     rng = np.random.default_rng(runs)
