@@ -99,3 +99,30 @@ def test_replace_keeps_the_sum_and_the_captured_graph(ext):
         k.close()
     finally:
         region.close()
+
+
+@pytest.mark.parametrize("n", [16384, 3000, 2])
+def test_sums_at_the_reference_sizes_are_member_sum_over_both_word_halves(ext, n):
+    """The reference's sizes (core/tests/test_slot_kernel.py:163-190) through the driver: three
+    rows in rank order, members N(0,1) from torch's generator, two calls in a row so that both
+    halves of the words (the sequence number's parity) carry a sum; each equals member_sum."""
+    region = Region.in_pinned_memory(ext, "host")
+    try:
+        region.set_members(RANKS, RANKS)
+        k = SlotKernel(region, 0, 0, ext=ext)
+        for call in (1, 2):
+            xs = {r: torch.randn(n, generator=torch.Generator().manual_seed(1000 * r + n + call))
+                  .to(torch.bfloat16) for r in RANKS}
+            for r in (1, 2):
+                put_words(region, r, xs[r], call)
+            x0 = xs[0].cuda()
+            out = torch.full_like(x0, float("nan"))
+            k.all_reduce_into(x0, out)
+            torch.cuda.synchronize()
+            assert np.array_equal(bits(out), oracle.member_sum([bits(xs[r]) for r in RANKS])), call
+        assert not k.can_take(torch.empty(3, dtype=torch.bfloat16, device="cuda"))  # odd
+        assert not k.can_take(torch.empty(4, dtype=torch.float16, device="cuda"))
+        assert not k.can_take(torch.empty(MAXN + 2, dtype=torch.bfloat16, device="cuda"))
+        k.close()
+    finally:
+        region.close()
