@@ -595,11 +595,29 @@ def bench_c4(ext, steps, warmup):
     ok_d = bool(torch.equal(back.view(torch.int16), rows[:4].view(torch.int16)))
     per_sort, _ = time_launches(lambda: ext.order_pairs(s, NB * BS, out=pairs), steps, warmup,
                                 stream)
+
+    # the same rows restored as a store's tables name them: one written range per layer, row t
+    # to slot t (scatter_ranges, what the Restorer launches, here over the whole cache at once)
+    starts = torch.zeros(1, dtype=torch.long, device=dev)
+    first_rows = torch.tensor([0, n], dtype=torch.long, device=dev)
+
+    def by_ranges():
+        ext.scatter_ranges(ptrs, starts, first_rows, n, heads, rows.data_ptr(), n, D, BS,
+                           strides, 2)
+
+    for t in caches[:4]:
+        t.zero_()
+    per_r, _ = time_launches(by_ranges, steps, warmup, stream)
+    in_order = torch.arange(n, dtype=torch.long, device=dev)
+    ext.gather_rows(ptrs[:4], in_order, heads, back.data_ptr(), n, D, BS, strides, 2)
+    torch.cuda.synchronize()
+    ok_r = bool(torch.equal(back.view(torch.int16), rows[:4].view(torch.int16)))
     del rows, caches, back
     torch.cuda.empty_cache()
     ms = sum(per) / len(per)
     ms_o = sum(per_o) / len(per_o)
     ms_d = sum(per_d) / len(per_d)
+    ms_r = sum(per_r) / len(per_r)
     return {
         "config": "C4 restore: [32,8,262144,2,128] bf16 rows into a fresh 16384-block cache, "
                   "random-permutation block table (64 seqs x 4096 tokens)",
@@ -624,6 +642,14 @@ def bench_c4(ext, steps, warmup):
             "frac_of_8tbs": round(2 * payload / ms_d / 1e6 / PEAK_HBM_GBS, 4),
             "sort_ms": round(sum(per_sort) / len(per_sort), 4),
             "round_trip_equal_first_4_layers": ok_d,
+        },
+        "by_ranges_in_slot_order": {
+            "how": "the same rows as a store's tables hold them, row t to slot t: one written "
+                   "range per layer through scatter_ranges (each XCD a contiguous part)",
+            "ms": round(ms_r, 3),
+            "gbs": round(2 * payload / ms_r / 1e6, 1),
+            "frac_of_8tbs": round(2 * payload / ms_r / 1e6 / PEAK_HBM_GBS, 4),
+            "round_trip_equal_first_4_layers": ok_r,
         },
     }
 
@@ -1260,7 +1286,9 @@ def pmc_workload(ext, which="gather", launches=5):
     read against.
 
     gather: the C2 gather. scatter: the C4 restore scatter (32 layers, 64 GiB moved). pairs: the
-    same restore in cache order (scatter_pairs, the pairs sorted by slot). reduce: the C5 local
+    same restore in cache order (scatter_pairs, the pairs sorted by slot). ranges: the same rows
+    restored as one written range per layer, slots 0..n-1 in order (scatter_ranges, as the
+    Restorer launches it, at C4's size). reduce: the C5 local
     reduce, each call on another of 32 buffer sets (1.1 GiB in all, over 4x what the Infinity
     Cache holds).
     """
@@ -1283,7 +1311,7 @@ def pmc_workload(ext, which="gather", launches=5):
             ext.gather_rows(ptrs, s, heads, out.data_ptr(), n, D, BS, strides, 2)
         algo = 2 * L * H * n * 2 * D * 2
         del layers, out
-    elif which in ("scatter", "pairs"):
+    elif which in ("scatter", "pairs", "ranges"):
         L, NB, BS, H, D = 32, 16384, 16, 8, 128
         n = NB * BS
         # the counters count bytes, whatever they hold: the rows are left uninitialised
@@ -1300,8 +1328,13 @@ def pmc_workload(ext, which="gather", launches=5):
 
             o_slots, o_rows = destination_order(slots, block_size=BS)
             os_dev, or_dev = torch.from_numpy(o_slots).to(dev), torch.from_numpy(o_rows).to(dev)
+        starts = torch.zeros(1, dtype=torch.long, device=dev)
+        first_rows = torch.tensor([0, n], dtype=torch.long, device=dev)
         for _ in range(launches):
-            if which == "pairs":
+            if which == "ranges":
+                ext.scatter_ranges(ptrs, starts, first_rows, n, heads, rows.data_ptr(), n, D, BS,
+                                   strides, 2)
+            elif which == "pairs":
                 ext.scatter_pairs(ptrs, os_dev, or_dev, heads, rows.data_ptr(), n, D, BS, strides,
                                   2)
             else:
@@ -1350,7 +1383,7 @@ def main(argv=None):
                     help="only the host copies of the path beside plain copies, for a "
                          "rocprofv3 memory-copy trace")
     ap.add_argument("--pmc", nargs="?", const="gather", default=None,
-                    choices=("gather", "scatter", "pairs", "reduce"),
+                    choices=("gather", "scatter", "pairs", "ranges", "reduce"),
                     help="only a counter run's workload: 5 calls of the named kernel (default "
                          "gather), then 5 calibration copies")
     a = ap.parse_args(argv)
