@@ -104,7 +104,8 @@ def describe(stage: str, layers: Sequence[int], heads: Sequence[HeadSlot], capac
         "layers": sorted(int(x) for x in layers),
         "heads": [int(h) for h in heads],
         "table_stride": HEAD_STRIDE,
-        "slots": [int(s) for s in slots],
+        "slots": (slots.astype(np.int64, copy=False).tolist() if isinstance(slots, np.ndarray)
+                  else [int(s) for s in slots]),
         "dtype": dtype,
         "shape": [2, head_dim],
     }
@@ -650,8 +651,8 @@ class StepStager:
             job.times["ready"] = t1 = time.perf_counter()
             self.stats["copy_s"] += t1 - t0
             self.stats["bytes_staged"] += len(g.filled) * heads * n * row_bytes
-            slots = st.host_slots[:n].tolist()
-            self.stats["bytes_sent"] += (sum(1 for x in slots if x >= 0) * row_bytes
+            slots = st.host_slots[:n].numpy()  # the descriptor copies them out
+            self.stats["bytes_sent"] += (int(np.count_nonzero(slots >= 0)) * row_bytes
                                          * len(g.filled) * heads)
             job.descriptor = describe(st.name, sorted(g.filled), g.heads, st.capacity,
                                       self.paged.head_dim, self._kernel.elem, slots,

@@ -7,6 +7,7 @@ the store reads (core/everserve/state/mirror.py:778-800). It is checked against 
 store derives (store/src/storage.rs:521-540), computed by hand for a small case.
 """
 
+import numpy as np
 import pytest
 import torch
 
@@ -36,6 +37,13 @@ def test_the_descriptor_is_the_oracles(layers, heads, cap, d, elem, dtype):
     got = staging.describe("stage3.rows", layers, heads, cap, d, elem, slots, dtype)
     want = oracle.staged_step("stage3.rows", layers, heads, cap, d, elem, slots, dtype)
     assert got == want
+    # slot ids handed over as a numpy array (the stager's pinned copy): the same descriptor,
+    # holding Python ints of its own
+    arr = np.array(slots, dtype=np.int64)
+    from_array = staging.describe("stage3.rows", layers, heads, cap, d, elem, arr, dtype)
+    assert from_array == want and all(type(x) is int for x in from_array["slots"])
+    arr[0] = 99
+    assert from_array["slots"][0] == 5
 
 
 def test_the_store_derives_the_offsets_of_the_layout():
