@@ -911,6 +911,7 @@ def bench_c5(ext, steps, warmup):
     del sets
     torch.cuda.empty_cache()
     decode = reduce_decode_sizes(ext, flags, order, state, steps, dev)
+    late = reduce_late_member(ext, dev)
     us = sum(per) / len(per) * 1e3
     algo = (K + 1) * N * 2
     return {
@@ -925,7 +926,68 @@ def bench_c5(ext, steps, warmup):
         "stalled_flag": {"timeout_ns": 1_000_000, "host_ms_to_return": round(abort_ms, 3),
                          "reason": (st >> 8) & 0xFF, "late_mask": st & 0xFF},
         "decode_sizes": decode,
+        "late_member": late,
     }
+
+
+def reduce_late_member(ext, dev, trials=15, spin_us=50):
+    """A call whose member in order position 4 (row 1) is still out when it starts, as when a
+    peer's push lands after the reduce is launched: the reduce runs on one stream; on another, a
+    bounded spin kernel (``torch.cuda._sleep``) and then a fill write that member's flag. The
+    figure is the time from the flag's write (an event after the fill) to the call's end (an
+    event after the reduce), median of ``trials``; every output is checked against the call with
+    every member in."""
+    import torch
+
+    from everserve_amd.kernels import REDUCE_STATE_WORDS
+
+    a, b = torch.cuda.Stream(device=dev), torch.cuda.Stream(device=dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(b):
+        torch.cuda._sleep(1000)
+        e0.record()
+        torch.cuda._sleep(1_000_000)
+        e1.record()
+    torch.cuda.synchronize()
+    cycles_per_us = 1_000_000 / (e0.elapsed_time(e1) * 1e3)
+    rows, late_row = [5, 3, 7, 0, 1, 6, 2, 4], 1
+    out = {"how": "order [5,3,7,0,1,6,2,4], row 1 late: its flag written by a fill on a second "
+                  f"stream after a {spin_us} us spin; microseconds from that write to the call's "
+                  "end"}
+    for n in (2048, 65536, 256 * 8192):
+        bufs = [torch.randn(n, device=dev).to(torch.bfloat16) for _ in range(8)]
+        table = torch.tensor([t.data_ptr() for t in bufs], dtype=torch.long, device=dev)
+        order = torch.tensor([8, *rows], dtype=torch.int32, device=dev)
+        flags = torch.ones(8, dtype=torch.long, device=dev)
+        state = torch.zeros(REDUCE_STATE_WORDS, dtype=torch.long, device=dev)
+        ref, y = (torch.empty(n, dtype=torch.bfloat16, device=dev) for _ in range(2))
+        ext.local_reduce(table, flags, order, ref, 1, 10**9, 0, state)
+        torch.cuda.synchronize()
+        us, equal, ok = [], True, True
+        for t in range(trials + 2):
+            epoch = 2 + t
+            flags.fill_(epoch)
+            flags[late_row] = epoch - 1
+            y.zero_()
+            torch.cuda.synchronize()
+            written, ended = (torch.cuda.Event(enable_timing=True) for _ in range(2))
+            with torch.cuda.stream(a):
+                ext.local_reduce(table, flags, order, y, epoch, 100_000_000, 0, state)
+                ended.record()
+            with torch.cuda.stream(b):
+                torch.cuda._sleep(int(spin_us * cycles_per_us))
+                flags[late_row:late_row + 1].fill_(epoch)
+                written.record()
+            torch.cuda.synchronize()
+            equal &= bool(torch.equal(y.view(torch.int16), ref.view(torch.int16)))
+            ok &= int(state[0].item()) == epoch << 16
+            if t >= 2:
+                us.append(written.elapsed_time(ended) * 1e3)
+        us.sort()
+        out[f"n{n}"] = {"us_flag_to_end": round(us[len(us) // 2], 2),
+                        "sum_equal_all_in": equal, "status_ok": ok}
+        del bufs
+    return out
 
 
 def reduce_decode_sizes(ext, flags, order, state, steps, dev, per_graph=50):

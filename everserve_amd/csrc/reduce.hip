@@ -19,6 +19,13 @@
 // Every workgroup is resident at once and bounds its own wait by ABORT and the clock, so they
 // give up together, within the skew of their starts.
 //
+// Early start (EVS_REDUCE_EARLY): a workgroup that finds a member missing at its first read of the
+// flags loads the members already in for its first pass before it waits, and after the wait loads
+// only the members that came in during it, into the registers that read zeros for them. Every
+// load still follows the observation of its member's flag, and the sum still runs in the member
+// order, so the result and the outcome equal those of waiting first. After a late flag, the call
+// then has only the late members' loads left instead of every member's.
+//
 // The call's outcome is one word, state[0] = (epoch << 16) | (reason << 8) | late rows, written by
 // the last workgroup to count. Each workgroup counts once its wait is over, before its payload:
 // the outcome is settled then, and state[0] is read only after the kernel has completed.
@@ -57,6 +64,8 @@ constexpr int kVpt = EVS_REDUCE_VPT;  // 8-element vectors per thread per pass
 constexpr int kMaxBlocks = EVS_REDUCE_MAX_BLOCKS;  // all resident on 256 CUs: each polls once
 constexpr int kPollsPerCheck = 32; // flag polls between clock and ABORT reads
 constexpr int kBadOrder = 4;       // reason bit: `order` named a row outside [0, MAX_ROWS)
+constexpr int kVectors = 1;        // mode bit: every member buffer 16-byte aligned
+constexpr int kEarly = 2;          // mode bit: early start (a member missing at the first read)
 constexpr int kDoneBits = 20;      // counting words: workgroups done in bits [0, 20), outcome above
 constexpr uint32_t kGroups = 8;    // group counting words
 constexpr int kGroupStride = 32;   // words between counting words (256 bytes)
@@ -73,6 +82,15 @@ static_assert(kGroupStride * (1 + kGroups) <= EVS_REDUCE_STATE_WORDS, "state rec
 #endif
 #ifndef EVS_REDUCE_FENCE
 #define EVS_REDUCE_FENCE 3
+#endif
+// Early start (1): a workgroup that finds a member missing at its first read of the flags loads
+// its first pass of the members already in, then waits, then loads only the late ones. 0: it
+// waits first and loads every member after the wait.
+#ifndef EVS_REDUCE_EARLY
+#define EVS_REDUCE_EARLY 1
+#endif
+#if EVS_REDUCE_EARLY && EVS_REDUCE_FENCE != 3
+#error "early start needs the coherent buffer loads (EVS_REDUCE_FENCE 3)"
 #endif
 // buffer-load cache policy: sc1 (coherent at agent scope), plus nt when the payload streams
 constexpr int kPayloadScope = 16 | ((EVS_REDUCE_NT & 1) ? 2 : 0);
@@ -147,171 +165,165 @@ __device__ __forceinline__ bool last(uint64_t* w, uint64_t before, uint32_t arri
   return true;
 }
 
-__global__ __launch_bounds__(kThreads) void local_reduce(ReduceArgs a) {
-  __shared__ const uint16_t* s_src[kMaxRows];  // member in order position q, or null: missing
-  __shared__ int s_count;
-  __shared__ int s_vectors;                      // every member buffer 16-byte aligned
-  __shared__ uint32_t s_outcome;                 // reason << 8 | late rows
-
-  const int tid = threadIdx.x;
-  if (tid < 64) {
-    const int lane = tid;
-    // One round of independent loads: the order words, the buffer table and every row's flag
-    // (lane r holds row r's), so a call whose members are all in costs one memory latency here.
-    const int o = lane <= kMaxRows ? a.order[lane] : 0;
-    const int64_t row_addr = lane < kMaxRows ? a.bufs[lane] : 0;
-    uint64_t row_flag = lane < kMaxRows ? load_system(a.flags + lane) : 0;
-    int count = __shfl(o, 0);
-    count = count < 0 ? 0 : (count > kMaxRows ? kMaxRows : count);
-    // lane q < count stands for the member in order position q
-    const int listed_row = __shfl(o, (1 + lane) & 63);
-    const bool listed = lane < count;
-    const int row = listed ? listed_row : -1;
-    const bool valid = listed && row >= 0 && row < kMaxRows;
-    uint32_t reason = __ballot(listed && !valid) ? kBadOrder : 0;
-    const int src_lane = valid ? row : 0;
-
-    // every lane takes part in every shuffle: a lane left out supplies no value to read
-    int ready = __shfl(static_cast<int>(row_flag == a.epoch), src_lane);
-    uint64_t missing = __ballot(valid && !ready);
-    bool named = false;
-    uint32_t late_rows = 0;
-    if (missing != 0) {
-      const int64_t t0 = wall_clock64();
-      for (uint64_t poll = 0;; ++poll) {
-        if (poll % kPollsPerCheck == kPollsPerCheck - 1) {
-          const int64_t waited = wall_clock64() - t0;
-          uint64_t abort = 0, bound_ns = 0;
-          if (lane == 0 && a.ctrl != nullptr) {
-            abort = load_system(reinterpret_cast<const uint64_t*>(a.ctrl + EVS_ABORT));
-            bound_ns = load_system(reinterpret_cast<const uint64_t*>(a.ctrl + EVS_BOUND));
-          }
-          abort = __shfl(abort, 0);
-          bound_ns = __shfl(bound_ns, 0);
-          // rows this workgroup still waits for
-          uint32_t rows = (missing >> lane) & 1 ? (1u << row) : 0u;
-          for (int q = 1; q < kMaxRows; q <<= 1) rows |= __shfl_xor(rows, q);
-          late_rows = rows;
-          const int64_t waited_ns = waited * 1000000 / a.clock_khz;
-          if (a.ctrl != nullptr && static_cast<int64_t>(bound_ns) > 0 &&
-              waited_ns > static_cast<int64_t>(bound_ns)) {
-            if (lane == 0) {
-              if (!named)
-                __hip_atomic_fetch_add(a.state + 3, uint64_t{1}, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-              // every check: another workgroup's clear may have raced this one's write
-              store_system(a.ctrl + EVS_LATE, static_cast<int64_t>(late_rows));
-            }
-            named = true;
-          }
-          if (abort != 0) {
-            reason |= EVS_REDUCE_ABORTED;
-            break;
-          }
-          if (waited > a.timeout_ticks || poll >= a.max_polls) {
-            reason |= EVS_REDUCE_TIMED_OUT;
-            break;
-          }
+// Wave 0: poll the flags until every wanted member is in (lane q wants the member in order
+// position q when `want`; bit q of `missing` is set while it is out), ABORT is set, or the timeout
+// passes. Returns the positions still missing. Past BOUND it names the rows still awaited in
+// LATE, and the last workgroup that named clears LATE once its wait is over. `reason` gains the
+// abort or timeout bit; `late_rows` is the rows still missing when the wait gave up.
+__device__ __forceinline__ uint64_t wait_members(const ReduceArgs& a, int lane, bool want,
+                                                 int src_lane, int row, uint64_t missing,
+                                                 uint32_t& reason, uint32_t& late_rows) {
+  bool named = false;
+  late_rows = 0;
+  const int64_t t0 = wall_clock64();
+  for (uint64_t poll = 0;; ++poll) {
+    if (poll % kPollsPerCheck == kPollsPerCheck - 1) {
+      const int64_t waited = wall_clock64() - t0;
+      uint64_t abort = 0, bound_ns = 0;
+      if (lane == 0 && a.ctrl != nullptr) {
+        abort = load_system(reinterpret_cast<const uint64_t*>(a.ctrl + EVS_ABORT));
+        bound_ns = load_system(reinterpret_cast<const uint64_t*>(a.ctrl + EVS_BOUND));
+      }
+      abort = __shfl(abort, 0);
+      bound_ns = __shfl(bound_ns, 0);
+      // rows this workgroup still waits for
+      uint32_t rows = (missing >> lane) & 1 ? (1u << row) : 0u;
+      for (int q = 1; q < kMaxRows; q <<= 1) rows |= __shfl_xor(rows, q);
+      late_rows = rows;
+      const int64_t waited_ns = waited * 1000000 / a.clock_khz;
+      if (a.ctrl != nullptr && static_cast<int64_t>(bound_ns) > 0 &&
+          waited_ns > static_cast<int64_t>(bound_ns)) {
+        if (lane == 0) {
+          if (!named)
+            __hip_atomic_fetch_add(a.state + 3, uint64_t{1}, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+          // every check: another workgroup's clear may have raced this one's write
+          store_system(a.ctrl + EVS_LATE, static_cast<int64_t>(late_rows));
         }
-        __builtin_amdgcn_s_sleep(2);
-        row_flag = lane < kMaxRows ? load_system(a.flags + lane) : 0;
-        ready = __shfl(static_cast<int>(row_flag == a.epoch), src_lane);
-        missing = __ballot(valid && !ready);
-        if (missing == 0) break;
+        named = true;
+      }
+      if (abort != 0) {
+        reason |= EVS_REDUCE_ABORTED;
+        break;
+      }
+      if (waited > a.timeout_ticks || poll >= a.max_polls) {
+        reason |= EVS_REDUCE_TIMED_OUT;
+        break;
       }
     }
-    if (missing == 0) late_rows = 0;
-    if (named && lane == 0) {
-      // the wait is over; the last workgroup that named clears the word
-      if (__hip_atomic_fetch_add(a.state + 3, ~uint64_t{0}, __ATOMIC_RELAXED,
-                                 __HIP_MEMORY_SCOPE_AGENT) == 1)
-        store_system(a.ctrl + EVS_LATE, 0);
-    }
-    const int64_t mapped_addr = __shfl(row_addr, src_lane);
-    const int64_t addr = valid ? mapped_addr : 0;
-    const bool unaligned = __ballot((addr & 15) != 0) != 0;
-    if (lane < kMaxRows) {
-      const bool have = valid && !((missing >> lane) & 1);
-      s_src[lane] = have ? reinterpret_cast<const uint16_t*>(addr) : nullptr;
-    }
-    if (lane == 0) {
-      s_count = count;
-      s_vectors = !unaligned;
-      s_outcome = (reason << 8) | late_rows;
-    }
-    // the flags were read with relaxed loads: order the payload reads after them
-    if (EVS_REDUCE_FENCE == 1) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    __builtin_amdgcn_s_sleep(2);
+    const uint64_t row_flag = lane < kMaxRows ? load_system(a.flags + lane) : 0;
+    const int ready = __shfl(static_cast<int>(row_flag == a.epoch), src_lane);
+    missing = __ballot(want && !ready);
+    if (missing == 0) break;
   }
-  __syncthreads();
-  if (EVS_REDUCE_FENCE == 2) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-  // This workgroup's outcome is settled once its wait is over, so it is counted now: the
-  // counting atomic's round trip then overlaps the payload instead of following it. state[0] is
-  // read only once the kernel has completed, when every workgroup's payload is written too.
-  const uint32_t groups = gridDim.x < kGroups ? gridDim.x : kGroups;
-  const uint32_t group = blockIdx.x % groups;
-  uint64_t* const group_word = a.state + kGroupStride * (1 + group);
-  uint64_t group_before = 0;
-  if (tid == 0) group_before = arrive(group_word, s_outcome);
+  if (missing == 0) late_rows = 0;
+  if (named && lane == 0) {
+    // the wait is over; the last workgroup that named clears the word
+    if (__hip_atomic_fetch_add(a.state + 3, ~uint64_t{0}, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT) == 1)
+      store_system(a.ctrl + EVS_LATE, 0);
+  }
+  return missing;
+}
 
-  const int count = s_count;
-  const int64_t nvec = s_vectors ? a.nvec : 0;
-  const uint16_t* src[kMaxRows];
+// The bytes a pass's buffer resources span from vector vb: the vectors left, at most 1 GiB.
+__device__ __forceinline__ int pass_records(int64_t nvec, int64_t vb) {
+  const int64_t left = (nvec - vb) * 16;
+  return static_cast<int>(left < (int64_t{1} << 30) ? left : (int64_t{1} << 30));
+}
+
+// One pass's payload loads: vector i of every member q, through q's resource (an absent member's
+// resource is empty, so its loads return zeros without touching memory).
+__device__ __forceinline__ void load_pass(u32x4 (&x)[kVpt][kMaxRows],
+                                          const __amdgpu_buffer_rsrc_t (&r)[kMaxRows], int tid) {
+  // vector-major (1): vector i's loads from every member come before vector i + 1's, so its sum
+  // and store can go out while the later vectors' loads are still in flight
 #pragma unroll
-  for (int q = 0; q < kMaxRows; q++) src[q] = q < count ? s_src[q] : nullptr;
+  for (int j = 0; j < kVpt * kMaxRows; j++) {
+    const int i = EVS_REDUCE_LOAD_ORDER ? j / kMaxRows : j % kVpt;
+    const int q = EVS_REDUCE_LOAD_ORDER ? j % kMaxRows : j / kVpt;
+    x[i][q] = __builtin_amdgcn_raw_buffer_load_b128(r[q], (i * kThreads + tid) * 16, 0,
+                                                    kPayloadScope);
+    // keep each vector's loads together, in this order (the scheduler would group them by
+    // member otherwise)
+    if (EVS_REDUCE_LOAD_ORDER && q == kMaxRows - 1) __builtin_amdgcn_sched_barrier(0);
+  }
+}
 
-  // vectors of 8 elements: one 16-byte load per member
+#if EVS_REDUCE_EARLY
+// An early start's second round: the vectors of each member q whose bit is set in `late` (the
+// same in every lane), loaded over the zeros the first round read for it. Only those members'
+// loads are issued, into the registers the first round filled, so the round needs none more.
+__device__ __forceinline__ void load_late(u32x4 (&x)[kVpt][kMaxRows],
+                                          const uint16_t* const (&late_src)[kMaxRows],
+                                          uint32_t late, int64_t vb, int records, int tid) {
+#pragma unroll
+  for (int q = 0; q < kMaxRows; q++) {
+    if ((late >> q) & 1) {
+      const __amdgpu_buffer_rsrc_t r = uniform_rsrc(late_src[q] + vb * 8, records);
+#pragma unroll
+      for (int i = 0; i < kVpt; i++)
+        x[i][q] = __builtin_amdgcn_raw_buffer_load_b128(r, (i * kThreads + tid) * 16, 0,
+                                                        kPayloadScope);
+    }
+  }
+}
+#endif
+
+// Each vector's sum over the members in order, in fp32 from +0.0, rounded to bf16 and stored
+// through the output resource `ro`, which ends at the last vector, so a store past it is dropped.
+// Adding an absent member's +0.0 changes no sum: the accumulator starts at +0.0 and so is never
+// -0.0. Straight-line, so each vector's sum waits only for its own loads.
+__device__ __forceinline__ void sum_store(const u32x4 (&x)[kVpt][kMaxRows],
+                                          __amdgpu_buffer_rsrc_t ro, int tid) {
+#pragma unroll
+  for (int i = 0; i < kVpt; i++) {
+    float acc[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) acc[e] = 0.0f;
+#pragma unroll
+    for (int q = 0; q < kMaxRows; q++) {
+#pragma unroll
+      for (int w = 0; w < 4; w++) {
+        acc[2 * w] += bf16_to_f32(x[i][q][w] & 0xffffu);
+        acc[2 * w + 1] += bf16_to_f32(x[i][q][w] >> 16);
+      }
+    }
+    u32x4 y;
+#pragma unroll
+    for (int w = 0; w < 4; w++)
+      y[w] = f32_to_bf16(acc[2 * w]) | (f32_to_bf16(acc[2 * w + 1]) << 16);
+    __builtin_amdgcn_raw_buffer_store_b128(y, ro, (i * kThreads + tid) * 16, 0, kOutputPolicy);
+    // the store goes out now, not after the last vector's sum
+    if (EVS_REDUCE_LOAD_ORDER) __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// The rest of a call from vector vb on: the passes of the vector path, the elements the vectors
+// do not cover, and the completion count.
+__device__ __forceinline__ void finish_call(const ReduceArgs& a,
+                                            const uint16_t* const (&src)[kMaxRows], int count,
+                                            int64_t nvec, int64_t vb, uint64_t* group_word,
+                                            uint64_t group_before, uint32_t group,
+                                            uint32_t groups) {
+  const int tid = threadIdx.x;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads * kVpt;
-  for (int64_t vb = static_cast<int64_t>(blockIdx.x) * kThreads * kVpt; vb < nvec; vb += stride) {
+  // vectors of 8 elements: one 16-byte load per member
+  for (; vb < nvec; vb += stride) {
     const int64_t v0 = vb + tid;
     u32x4 x[kVpt][kMaxRows];
     if (EVS_REDUCE_FENCE == 3) {
-      // a buffer resource per member over this pass's vectors: a load past the end returns 0
-      const int64_t left = (nvec - vb) * 16;
-      const int records = static_cast<int>(left < (int64_t{1} << 30) ? left : (int64_t{1} << 30));
-      // an absent member (missing, or past the count) gets an empty resource: its loads return
-      // zeros without touching memory, so no branch separates the loads from their uses
+      // a buffer resource per member over this pass's vectors: a load past the end returns 0;
+      // an absent member (missing, or past the count) gets an empty resource, so no branch
+      // separates the loads from their uses
+      const int records = pass_records(nvec, vb);
       __amdgpu_buffer_rsrc_t r[kMaxRows];
 #pragma unroll
       for (int q = 0; q < kMaxRows; q++)
         r[q] = src[q] != nullptr ? uniform_rsrc(src[q] + vb * 8, records) : uniform_rsrc(a.out, 0);
-      // vector-major (1): vector i's loads from every member come before vector i + 1's, so its
-      // sum and store can go out while the later vectors' loads are still in flight
-#pragma unroll
-      for (int j = 0; j < kVpt * kMaxRows; j++) {
-        const int i = EVS_REDUCE_LOAD_ORDER ? j / kMaxRows : j % kVpt;
-        const int q = EVS_REDUCE_LOAD_ORDER ? j % kMaxRows : j / kVpt;
-        x[i][q] = __builtin_amdgcn_raw_buffer_load_b128(r[q], (i * kThreads + tid) * 16, 0,
-                                                        kPayloadScope);
-        // keep each vector's loads together, in this order (the scheduler would group them by
-        // member otherwise)
-        if (EVS_REDUCE_LOAD_ORDER && q == kMaxRows - 1) __builtin_amdgcn_sched_barrier(0);
-      }
-      // the sums and stores, straight-line: adding an absent member's +0.0 changes no sum (the
-      // accumulator starts at +0.0 and so is never -0.0), and the output resource ends at the
-      // last vector, so a store past it is dropped
-      const __amdgpu_buffer_rsrc_t ro = uniform_rsrc(a.out + vb * 8, records);
-#pragma unroll
-      for (int i = 0; i < kVpt; i++) {
-        float acc[8];
-#pragma unroll
-        for (int e = 0; e < 8; e++) acc[e] = 0.0f;
-#pragma unroll
-        for (int q = 0; q < kMaxRows; q++) {
-#pragma unroll
-          for (int w = 0; w < 4; w++) {
-            acc[2 * w] += bf16_to_f32(x[i][q][w] & 0xffffu);
-            acc[2 * w + 1] += bf16_to_f32(x[i][q][w] >> 16);
-          }
-        }
-        u32x4 y;
-#pragma unroll
-        for (int w = 0; w < 4; w++)
-          y[w] = f32_to_bf16(acc[2 * w]) | (f32_to_bf16(acc[2 * w + 1]) << 16);
-        __builtin_amdgcn_raw_buffer_store_b128(y, ro, (i * kThreads + tid) * 16, 0,
-                                               kOutputPolicy);
-        // the store goes out now, not after the last vector's sum
-        if (EVS_REDUCE_LOAD_ORDER) __builtin_amdgcn_sched_barrier(0);
-      }
+      load_pass(x, r, tid);
+      sum_store(x, uniform_rsrc(a.out + vb * 8, records), tid);
       continue;
     } else {
 #pragma unroll
@@ -377,6 +389,127 @@ __global__ __launch_bounds__(kThreads) void local_reduce(ReduceArgs a) {
                          __HIP_MEMORY_SCOPE_SYSTEM);
     }
   }
+}
+
+__global__ __launch_bounds__(kThreads) void local_reduce(ReduceArgs a) {
+  __shared__ const uint16_t* s_src[kMaxRows];  // member in order position q, or null: missing
+  __shared__ int s_count;
+  __shared__ int s_mode;                         // kVectors | kEarly
+  __shared__ uint32_t s_outcome;                 // reason << 8 | late rows
+
+  const int tid = threadIdx.x;
+  const int64_t first_vb = static_cast<int64_t>(blockIdx.x) * kThreads * kVpt;  // first vector
+  // wave 0's view of the members (lane q: order position q), kept for an early start's wait
+  int row = -1, src_lane = 0;
+  bool valid = false;
+  int64_t addr = 0;
+  uint64_t missing = 0;
+  uint32_t reason = 0;
+  if (tid < 64) {
+    const int lane = tid;
+    // One round of independent loads: the order words, the buffer table and every row's flag
+    // (lane r holds row r's), so a call whose members are all in costs one memory latency here.
+    const int o = lane <= kMaxRows ? a.order[lane] : 0;
+    const int64_t row_addr = lane < kMaxRows ? a.bufs[lane] : 0;
+    const uint64_t row_flag = lane < kMaxRows ? load_system(a.flags + lane) : 0;
+    int count = __shfl(o, 0);
+    count = count < 0 ? 0 : (count > kMaxRows ? kMaxRows : count);
+    // lane q < count stands for the member in order position q
+    const int listed_row = __shfl(o, (1 + lane) & 63);
+    const bool listed = lane < count;
+    row = listed ? listed_row : -1;
+    valid = listed && row >= 0 && row < kMaxRows;
+    reason = __ballot(listed && !valid) ? kBadOrder : 0;
+    src_lane = valid ? row : 0;
+
+    // every lane takes part in every shuffle: a lane left out supplies no value to read
+    const int ready = __shfl(static_cast<int>(row_flag == a.epoch), src_lane);
+    missing = __ballot(valid && !ready);
+    const int64_t mapped_addr = __shfl(row_addr, src_lane);
+    addr = valid ? mapped_addr : 0;
+    const bool unaligned = __ballot((addr & 15) != 0) != 0;
+    // Early start: with a member missing, every wave loads this workgroup's first pass of the
+    // members already in, and this wave waits for the rest after issuing its share.
+    const bool early = EVS_REDUCE_EARLY && missing != 0 && !unaligned && first_vb < a.nvec;
+    uint32_t late_rows = 0;
+    if (missing != 0 && !early)
+      missing = wait_members(a, lane, valid, src_lane, row, missing, reason, late_rows);
+    if (lane < kMaxRows) {
+      const bool have = valid && !((missing >> lane) & 1);
+      s_src[lane] = have ? reinterpret_cast<const uint16_t*>(addr) : nullptr;
+    }
+    if (lane == 0) {
+      s_count = count;
+      s_mode = (unaligned ? 0 : kVectors) | (early ? kEarly : 0);
+      s_outcome = (reason << 8) | late_rows;
+    }
+    // the flags were read with relaxed loads: order the payload reads after them
+    if (EVS_REDUCE_FENCE == 1) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  }
+  __syncthreads();
+  if (EVS_REDUCE_FENCE == 2) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  // This workgroup's outcome is settled once its wait is over, so it is counted then: the
+  // counting atomic's round trip then overlaps the payload instead of following it. state[0] is
+  // read only once the kernel has completed, when every workgroup's payload is written too.
+  const uint32_t groups = gridDim.x < kGroups ? gridDim.x : kGroups;
+  const uint32_t group = blockIdx.x % groups;
+  uint64_t* const group_word = a.state + kGroupStride * (1 + group);
+  uint64_t group_before = 0;
+  const int mode = s_mode;
+  const bool waiting = EVS_REDUCE_EARLY && (mode & kEarly) != 0;
+  if (tid == 0 && !waiting) group_before = arrive(group_word, s_outcome);
+
+  const int count = s_count;
+  const int64_t nvec = (mode & kVectors) ? a.nvec : 0;
+  int64_t vb = first_vb;
+  const uint16_t* src[kMaxRows];
+#pragma unroll
+  for (int q = 0; q < kMaxRows; q++) src[q] = q < count ? s_src[q] : nullptr;
+#if EVS_REDUCE_EARLY
+  __shared__ const uint16_t* s_late[kMaxRows];  // member q if it came in during the wait
+  __shared__ uint32_t s_came;                     // the order positions s_late names
+  // unlikely: the call whose members are all in at the first read does not run this
+  if (__builtin_expect(waiting, 0)) {
+    // The first pass in two rounds of loads: the members that were in at the first read, issued
+    // now, and after the wait the members that came in during it. A member that never came in
+    // reads as zeros in both. The wait ends on the same events as the one above, so the outcome
+    // and the sum equal a wait-then-load call's.
+    u32x4 x[kVpt][kMaxRows];
+    const int records = pass_records(nvec, vb);
+    __amdgpu_buffer_rsrc_t r[kMaxRows];
+#pragma unroll
+    for (int q = 0; q < kMaxRows; q++)
+      r[q] = src[q] != nullptr ? uniform_rsrc(src[q] + vb * 8, records) : uniform_rsrc(a.out, 0);
+    load_pass(x, r, tid);
+    if (tid < 64) {
+      const int lane = tid;
+      uint32_t late_rows = 0;
+      const uint64_t still = wait_members(a, lane, valid && ((missing >> lane) & 1), src_lane,
+                                          row, missing, reason, late_rows);
+      const uint64_t came = missing & ~still;  // positions that came in during the wait
+      if (lane < kMaxRows)
+        s_late[lane] = (came >> lane) & 1 ? reinterpret_cast<const uint16_t*>(addr) : nullptr;
+      if (lane == 0) {
+        s_came = static_cast<uint32_t>(came);
+        s_outcome = (reason << 8) | late_rows;
+      }
+    }
+    __syncthreads();
+    if (tid == 0) group_before = arrive(group_word, s_outcome);
+    load_late(x, s_late, __builtin_amdgcn_readfirstlane(s_came), vb, records, tid);
+    sum_store(x, uniform_rsrc(a.out + vb * 8, records), tid);
+    vb += static_cast<int64_t>(gridDim.x) * kThreads * kVpt;
+    // the later passes and the element tail read every member that is in; this path ends here,
+    // so the common path's code stays as it is
+#pragma unroll
+    for (int q = 0; q < kMaxRows; q++)
+      if (src[q] == nullptr) src[q] = s_late[q];
+    finish_call(a, src, count, nvec, vb, group_word, group_before, group, groups);
+    return;
+  }
+#endif
+
+  finish_call(a, src, count, nvec, vb, group_word, group_before, group, groups);
 }
 
 int64_t g_clock_khz[64];

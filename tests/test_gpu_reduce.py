@@ -5,8 +5,11 @@ reference's sizes {16384, 3000, 2} (core/tests/test_slot_kernel.py:40) and at C5
 256 x 8192); the order-sensitive inputs of core/tests/test_slot_kernel.py:50-55; and the bounded
 wait: a stalled flag ends in a timeout naming that row, the host's ABORT word releases the wait,
 the LATE word names the stalled row while the wait passes BOUND and is cleared after, and a flag
-that arrives late (host-mapped, written by the host mid-wait) completes the call normally. Every
-wait in these tests is bounded by the kernel's own timeout.
+that arrives late (host-mapped, written by the host mid-wait) completes the call normally. A
+workgroup that finds members missing loads the others before it waits (early start): members
+that arrive late in the middle of the order, over several passes and an element tail, and one
+that never arrives, are summed exactly as a call that waited first. Every wait in these tests is
+bounded by the kernel's own timeout.
 """
 
 import ctypes
@@ -193,6 +196,51 @@ def test_a_flag_that_arrives_late_completes_the_call(ext):
         assert np.array_equal(bits(m.out), want)
     finally:
         ext.host_free(flags_host)
+
+
+@pytest.mark.parametrize("n", [256 * 8192, 2 * 1024 * 256 * 4 * 8 + 8 * 3 + 5])
+def test_members_that_arrive_late_in_the_middle_of_the_order(ext, n):
+    """Rows 0 and 6 sit mid-order and arrive one after the other while the call waits. A
+    workgroup loads the members already in before it waits, so the late ones are summed in their
+    order positions among them. The second size takes three passes of the grid and ends in an
+    element tail."""
+    flags_host, flags_dev = ext.host_alloc_mapped(MAXW * 8)
+    try:
+        words = (ctypes.c_int64 * MAXW).from_address(flags_host)
+        order = [5, 3, 7, 0, 1, 6, 2, 4]
+        inputs = {r: bf16_input(60 + r, n) for r in order}
+        m = Members(inputs, order)
+        for r in order:
+            words[r] = 0 if r in (0, 6) else 9
+        ext.local_reduce(m.bufs, flags_dev, m.order, m.out, 9, 3_000_000_000, 0, m.state)
+        time.sleep(0.01)
+        words[6] = 9
+        time.sleep(0.01)
+        words[0] = 9
+        torch.cuda.synchronize()
+        assert m.status() == (9, 0, 0)
+        want = oracle.member_sum([bits(inputs[r]) for r in order])
+        assert np.array_equal(bits(m.out), want)
+    finally:
+        ext.host_free(flags_host)
+
+
+def test_a_late_member_that_never_comes_reads_as_zeros_mid_order(ext):
+    """A member missing at the first read and never arriving: the members loaded before the wait
+    are summed with zeros in its place, and the timeout names it."""
+    n = 256 * 8192 + 13
+    order = [2, 7, 4, 1]
+    inputs = {r: bf16_input(80 + r, n) for r in order}
+    m = Members(inputs, order)
+    m.publish(epoch=5)
+    m.publish(epoch=4, rows=[4])
+    ext.local_reduce(m.bufs, m.flags, m.order, m.out, 5, 1_000_000, 0, m.state)  # 1 ms
+    torch.cuda.synchronize()
+    assert m.status() == (5, 2, 1 << 4)
+    want, reason, late = oracle.reduce_protocol({r: bits(x) for r, x in inputs.items()},
+                                                {r: (4 if r == 4 else 5) for r in order}, order, 5)
+    assert (reason, late) == (2, 1 << 4)
+    assert np.array_equal(bits(m.out), want)
 
 
 def test_a_captured_reduction_replays_like_eager_calls(ext):
