@@ -7,8 +7,12 @@
 // One call at a time has the set; a call that finds it busy (another thread of the process is in
 // a call) runs its shares on threads of its own instead, so callers never wait for each other.
 // The set is never destroyed: its threads sleep until the process ends, and nothing in it runs
-// at exit.
+// at exit. A child made by fork() inherits the set without its threads, and perhaps with its
+// lock held by a thread that is not there: a call in any process other than the one that made
+// the set runs on threads of its own and never touches the set.
 #pragma once
+
+#include <unistd.h>
 
 #include <condition_variable>
 #include <functional>
@@ -31,6 +35,10 @@ class Workers {
   void run(int n, const std::function<void(int)>& fn) {
     if (n <= 1) {
       if (n == 1) fn(0);
+      return;
+    }
+    if (getpid() != owner_) {  // a forked child: the set's threads are the parent's
+      run_on_own_threads(n, fn);
       return;
     }
     std::unique_lock<std::mutex> mine(call_, std::try_to_lock);
@@ -64,7 +72,7 @@ class Workers {
   }
 
  private:
-  Workers() = default;
+  Workers() : owner_(getpid()) {}
 
   static void run_on_own_threads(int n, const std::function<void(int)>& fn) {
     std::vector<std::thread> own;
@@ -97,6 +105,7 @@ class Workers {
     }
   }
 
+  const pid_t owner_;  // the process whose threads the set holds
   std::mutex call_;  // held by the call that has the set
   std::mutex m_;     // guards everything below
   std::condition_variable wake_, done_;

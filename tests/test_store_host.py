@@ -252,3 +252,63 @@ def test_store_tables_refuse_a_slot_outside_and_a_changed_row_size(ext):
     stage3, desc3 = staged([0], [0], 8, 4, 2, [1], seed=5)
     with pytest.raises(ValueError, match="bytes"):
         store.commit(stage3, desc3, 2)
+
+
+def test_a_forked_child_commits_while_the_parent_is_busy(ext):
+    """The library's host worker set belongs to the process that started it. A child forked
+    while the parent's threads are in commits (so the set may be mid-call, its lock held by a
+    thread the child does not have) commits on threads of its own and gets the store's bytes."""
+    import os
+    import threading
+    import time
+
+    num_slots, d, elem = 4096, 64, 2
+    stage, desc = staged([0, 1, 2, 3], [0, 1], 1024, d, elem, list(range(1024)), seed=11)
+    stop = threading.Event()
+
+    def busy():
+        state = ({"rows": {}, "steps": {}, "crc": {}}, {"rows": {}, "steps": {}, "crc": {}})
+        step = 1
+        while not stop.is_set():
+            commit_both(ext, stage, desc, num_slots, step, 8, state)
+            step += 1
+
+    commit_both(ext, stage, desc, num_slots, 1, 8, ({"rows": {}, "steps": {}, "crc": {}},
+                                                    {"rows": {}, "steps": {}, "crc": {}}))
+    worker = threading.Thread(target=busy)
+    worker.start()
+    children = []
+    try:
+        for _ in range(4):
+            time.sleep(0.02)
+            pid = os.fork()
+            if pid == 0:  # the child: one commit on 4 threads, checked against the oracle
+                code = 1
+                try:
+                    ours = {"rows": {}, "steps": {}, "crc": {}}
+                    theirs = {"rows": {}, "steps": {}, "crc": {}}
+                    commit_both(ext, stage, desc, num_slots, 3, 4, (ours, theirs))
+                    same = all(np.array_equal(ours[k][t], theirs[k][t])
+                               for k in ours for t in theirs[k])
+                    code = 0 if same else 2
+                finally:
+                    os._exit(code)
+            children.append(pid)
+    finally:
+        stop.set()
+        worker.join()
+    deadline = time.monotonic() + 60
+    codes = {}
+    while len(codes) < len(children) and time.monotonic() < deadline:
+        for pid in children:
+            if pid not in codes:
+                got, status = os.waitpid(pid, os.WNOHANG)
+                if got == pid:
+                    codes[pid] = os.waitstatus_to_exitcode(status)
+        time.sleep(0.01)
+    for pid in children:
+        if pid not in codes:  # a child that hung: end it, and fail
+            os.kill(pid, 9)
+            os.waitpid(pid, 0)
+    assert len(codes) == len(children), "a forked child did not finish its commit"
+    assert all(c == 0 for c in codes.values()), codes
