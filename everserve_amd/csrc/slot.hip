@@ -24,6 +24,13 @@
 // of this thread has not arrived (slot.cu:176-199). A counter after the sequence counters holds
 // the workgroups that named; the last to finish clears LATE. When a wait ends without a member,
 // that member's missing words are summed as zeros.
+//
+// The launch is laid out for latency. Wave 0 reads the sequence counter, the order words and the
+// buffer table in one round of independent loads, one lane a word, while every thread loads its
+// input; the lanes then resolve, per order position, where the member's words are read and (push)
+// where this member's go, into LDS. A poll issues the loads of every member of a batch back to
+// back from those addresses and waits once, and a batch is every member (up to 8) at 1 or 2 words
+// a thread, so a call of 8 members waits for one round trip a poll, not one per member.
 
 #include "common.hpp"
 
@@ -34,9 +41,16 @@ int wall_clock_khz(int64_t* khz);  // reduce.hip
 namespace {
 
 constexpr int kSlotThreads = 256;
-constexpr int kBatch = 4;          // members whose words a thread keeps in flight together
 constexpr int kMaxRows = EVS_MAX_ROWS;
 constexpr uint32_t kCheckEvery = 1024;
+
+// Members whose words a thread waits on together: every member at up to 8 words a thread (at most
+// 128 VGPRs of words), 4 at 16. One round of loads then covers a whole batch, so a call of k <= 8
+// members at decode sizes waits for one round trip, not one a batch.
+template <int W>
+constexpr int batch_of() {
+  return W <= 2 ? kMaxRows : 4;
+}
 
 struct SlotArgs {
   const uint32_t* x;        // the member's input, as pairs of bf16
@@ -61,64 +75,103 @@ __device__ __forceinline__ void store_sys(uint64_t* p, uint64_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
+// A value the same in every lane, moved to scalar registers.
+template <typename T>
+__device__ __forceinline__ T* uniform_ptr(T* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
+  return reinterpret_cast<T*>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
 __device__ __forceinline__ uint32_t to_bf16(float f) {
   const uint32_t u = __float_as_uint(f);
   if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
   return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
 }
 
-// The address of member m's words as this member reads them; parity_off is (seq & 1) * maxn2,
-// the word offset of this call's half.
-template <bool kPush>
-__device__ __forceinline__ const uint64_t* words_of(const SlotArgs& a, int m, size_t parity_off) {
-  if (kPush)
-    return reinterpret_cast<const uint64_t*>(a.bufs[a.my]) + parity_off * kMaxRows +
-           static_cast<size_t>(m) * a.maxn2;
-  return reinterpret_cast<const uint64_t*>(a.bufs[m]) + parity_off;
-}
-
 template <int W, bool kPush>
 __global__ __launch_bounds__(kSlotThreads) void slot_all_reduce(SlotArgs a) {
+  constexpr int kBatch = batch_of<W>();
+  // per order position q: the words this member reads (member q's, this call's parity half) and,
+  // for push, where it writes its own into member q's buffer; null for a row out of range
+  __shared__ const uint64_t* s_src[kMaxRows];
+  __shared__ uint64_t* s_dst[kMaxRows];
+  __shared__ uint64_t* s_mine;  // pull: this member's own half, where it publishes
+  __shared__ int s_row[kMaxRows];
   __shared__ uint32_t s_seq;
   __shared__ int s_n;
-  __shared__ int s_order[kMaxRows];
-  if (threadIdx.x == 0) {
-    const int64_t s = a.seqs[blockIdx.x] + 1;
-    a.seqs[blockIdx.x] = s;
-    s_seq = static_cast<uint32_t>(s);
-    int n = a.order[0];
+
+  const int b0 = blockIdx.x * W * kSlotThreads + threadIdx.x;
+  // the input, read before the prologue's loads return: nothing it depends on is pending
+  uint32_t xin[W];
+#pragma unroll
+  for (int j = 0; j < W; j++) {
+    const int i = b0 + j * kSlotThreads;
+    xin[j] = i < a.n2 ? a.x[i] : 0u;
+  }
+
+  if (threadIdx.x < 64) {
+    // One round of independent loads, one lane a word: this workgroup's sequence counter, the
+    // order words and the buffer table.
+    const int lane = threadIdx.x;
+    const int64_t prev =
+        lane == 0 ? static_cast<int64_t>(__hip_atomic_load(
+                        reinterpret_cast<const uint64_t*>(a.seqs + blockIdx.x), __ATOMIC_RELAXED,
+                        __HIP_MEMORY_SCOPE_AGENT))
+                  : 0;
+    const int o = lane <= kMaxRows ? a.order[lane] : 0;
+    const int64_t buf = lane < kMaxRows ? a.bufs[lane] : 0;
+    const int64_t s = __shfl(prev, 0) + 1;
+    if (lane == 0) a.seqs[blockIdx.x] = s;
+    const uint32_t seq = static_cast<uint32_t>(s);
+    const size_t parity_off = static_cast<size_t>(seq & 1u) * static_cast<size_t>(a.maxn2);
+    int n = __shfl(o, 0);
     n = n < 0 ? 0 : (n > kMaxRows ? kMaxRows : n);
-    s_n = n;
-    for (int q = 0; q < n; q++) {
-      const int r = a.order[1 + q];
-      s_order[q] = (r >= 0 && r < kMaxRows) ? r : -1;  // a row out of range is never waited for
+    // lane q < n stands for order position q; a row out of range is never waited for
+    const int r = __shfl(o, (lane + 1) & 63);
+    const bool valid = lane < n && r >= 0 && r < kMaxRows;
+    const int64_t their = __shfl(buf, valid ? r : 0);
+    const int64_t mine = __shfl(buf, a.my);
+    if (lane < kMaxRows) {
+      const uint64_t* src =
+          kPush ? reinterpret_cast<const uint64_t*>(mine) + parity_off * kMaxRows +
+                      static_cast<size_t>(r) * a.maxn2
+                : reinterpret_cast<const uint64_t*>(their) + parity_off;
+      s_src[lane] = valid ? src : nullptr;
+      s_dst[lane] = valid && kPush ? reinterpret_cast<uint64_t*>(their) + parity_off * kMaxRows +
+                                         static_cast<size_t>(a.my) * a.maxn2
+                               : nullptr;
+      s_row[lane] = valid ? r : -1;
+    }
+    if (lane == 0) {
+      s_seq = seq;
+      s_n = n;
+      s_mine = reinterpret_cast<uint64_t*>(mine) + parity_off;
     }
   }
   __syncthreads();
   const uint32_t seq = s_seq;
-  const size_t parity_off = static_cast<size_t>(seq & 1u) * static_cast<size_t>(a.maxn2);
   const int nmem = s_n;
-  const int b0 = blockIdx.x * W * kSlotThreads + threadIdx.x;
   const uint64_t tag = static_cast<uint64_t>(seq) << 32;
 
   // publish this member's words
   if (kPush) {
-    const size_t at = parity_off * kMaxRows + static_cast<size_t>(a.my) * a.maxn2;
     for (int q = 0; q < nmem; q++) {
-      if (s_order[q] < 0) continue;
-      uint64_t* dst = reinterpret_cast<uint64_t*>(a.bufs[s_order[q]]) + at;
+      uint64_t* dst = uniform_ptr(s_dst[q]);
+      if (dst == nullptr) continue;
 #pragma unroll
       for (int j = 0; j < W; j++) {
         const int i = b0 + j * kSlotThreads;
-        if (i < a.n2) store_sys(dst + i, tag | a.x[i]);
+        if (i < a.n2) store_sys(dst + i, tag | xin[j]);
       }
     }
   } else {
-    uint64_t* mine = reinterpret_cast<uint64_t*>(a.bufs[a.my]) + parity_off;
+    uint64_t* mine = uniform_ptr(s_mine);
 #pragma unroll
     for (int j = 0; j < W; j++) {
       const int i = b0 + j * kSlotThreads;
-      if (i < a.n2) store_sys(mine + i, tag | a.x[i]);
+      if (i < a.n2) store_sys(mine + i, tag | xin[j]);
     }
   }
 
@@ -138,14 +191,16 @@ __global__ __launch_bounds__(kSlotThreads) void slot_all_reduce(SlotArgs a) {
   uint64_t* late_count = reinterpret_cast<uint64_t*>(a.seqs + a.late_index);
 
   for (int b = 0; b < nmem; b += kBatch) {
+    const uint64_t* src[kBatch];
     int ms[kBatch];
     const int nm = nmem - b < kBatch ? nmem - b : kBatch;
     uint64_t w[kBatch][W];
     uint32_t todo[kBatch];
 #pragma unroll
     for (int q = 0; q < kBatch; q++) {
-      ms[q] = q < nm ? s_order[b + q] : -1;
-      todo[q] = (q < nm && ms[q] >= 0 && !released) ? valid : 0u;
+      src[q] = q < nm ? uniform_ptr(s_src[b + q]) : nullptr;
+      ms[q] = q < nm ? __builtin_amdgcn_readfirstlane(s_row[b + q]) : -1;
+      todo[q] = (src[q] != nullptr && !released) ? valid : 0u;
 #pragma unroll
       for (int j = 0; j < W; j++) w[q][j] = 0ull;
     }
@@ -153,10 +208,9 @@ __global__ __launch_bounds__(kSlotThreads) void slot_all_reduce(SlotArgs a) {
 #pragma unroll
       for (int q = 0; q < kBatch; q++) {
         if (!todo[q]) continue;
-        const uint64_t* p = words_of<kPush>(a, ms[q], parity_off) + b0;
 #pragma unroll
         for (int j = 0; j < W; j++)
-          if (todo[q] >> j & 1) w[q][j] = load_sys(p + j * kSlotThreads);
+          if (todo[q] >> j & 1) w[q][j] = load_sys(src[q] + b0 + j * kSlotThreads);
       }
       uint32_t any = 0;
 #pragma unroll
@@ -178,15 +232,17 @@ __global__ __launch_bounds__(kSlotThreads) void slot_all_reduce(SlotArgs a) {
         if (watch) {
           const int64_t bound = static_cast<int64_t>(load_sys(c + EVS_BOUND));
           if (bound > 0 && waited * 1000000 / a.clock_khz > bound) {
+            // the rows of this batch it still waits on, and of the batches after it, the rows
+            // whose first word of this thread has not arrived
             int64_t late = 0;
 #pragma unroll
             for (int q = 0; q < kBatch; q++)
               if (todo[q]) late |= int64_t{1} << ms[q];
             for (int q = b + nm; q < nmem; q++) {
-              const int m = s_order[q];
-              if (m < 0) continue;
-              if (static_cast<uint32_t>(load_sys(words_of<kPush>(a, m, parity_off) + b0) >> 32) != seq)
-                late |= int64_t{1} << m;
+              const uint64_t* p = s_src[q];
+              if (p == nullptr) continue;
+              if (static_cast<uint32_t>(load_sys(p + b0) >> 32) != seq)
+                late |= int64_t{1} << s_row[q];
             }
             if (!counted) {
               __hip_atomic_fetch_add(late_count, uint64_t{1}, __ATOMIC_RELAXED,
@@ -199,7 +255,7 @@ __global__ __launch_bounds__(kSlotThreads) void slot_all_reduce(SlotArgs a) {
       }
       __builtin_amdgcn_s_sleep(1);
     }
-    // sum the batch in order; a word that never arrived counts as zero
+    // sum the batch in order; a word that never arrived, or a row out of range, counts as zero
 #pragma unroll
     for (int q = 0; q < kBatch; q++) {
       if (q >= nm) continue;
