@@ -5,9 +5,10 @@ the members' words are staged in HBM instead: written by the test with the call'
 (as core/tests/test_slot_kernel.py:108-122 writes a cut-short push), or written by other members'
 kernels running at the same time on other streams. Checked bit for bit against
 core/everserve/reference/arith/ops.py:63-73 at the reference's sizes {16384, 3000, 2}, both
-variants, 1 and 16 words per thread, the order-sensitive inputs, a member that never arrives (named
-in LATE, released by ABORT, LATE cleared after), and replays of a captured graph whose sequence
-numbers advance in device memory. Every wait is bounded by the kernel's own timeout.
+variants, 1 and 16 words per thread, the order-sensitive inputs, eight members polled in one batch
+or two, an order entry out of range, a member that never arrives (named in LATE, released by
+ABORT, LATE cleared after), and replays of a captured graph whose sequence numbers advance in
+device memory. Every wait is bounded by the kernel's own timeout.
 """
 
 import ctypes
@@ -116,6 +117,49 @@ def test_the_sum_is_member_sum_in_rank_order(ext, push, n, words):
         out = reduce(ext, reg, 0, order, seqs, ys[0], words)
         torch.cuda.synchronize()
         assert np.array_equal(bits(out), oracle.member_sum([bits(ys[r]) for r in rows]))
+    finally:
+        reg.close()
+
+
+@pytest.mark.parametrize("push", [False, True])
+@pytest.mark.parametrize("words", [1, 2, 4, 16])
+def test_eight_members_in_one_batch_or_two(ext, push, words):
+    """Eight members in a shuffled order, this member (row 3) in the middle: at 1 or 2 words a
+    thread a poll covers all eight, at 4 or 16 they come in two batches of four. Two calls, so
+    both parity halves are used."""
+    rows = [5, 2, 7, 3, 0, 6, 1, 4]
+    n = 16384 if words < 16 else 2 * 16 * 256 * 2 + 6  # 16 words: several workgroups, a ragged end
+    reg = Region(ext, push, range(MAXW))
+    try:
+        order, seqs = reg.member(rows)
+        for seq in (1, 2):
+            xs = {r: member_input(100 * seq + r, n) for r in rows}
+            for r in rows:
+                if r != 3:
+                    reg.stage(3, r, xs[r], seq=seq)
+            out = reduce(ext, reg, 3, order, seqs, xs[3], words)
+            torch.cuda.synchronize()
+            want = oracle.member_sum([bits(xs[r]) for r in rows])
+            assert np.array_equal(bits(out), want), seq
+    finally:
+        reg.close()
+
+
+def test_a_row_out_of_range_in_the_order_is_skipped(ext):
+    """An order entry outside [0, 8) is never waited for and adds nothing; the members around it
+    are summed in their order."""
+    n, rows = 3000, [0, 1, 2]
+    reg = Region(ext, False, rows)
+    try:
+        o = torch.tensor([4, 2, 11, 0, 1] + [0] * (MAXW - 4), dtype=torch.int32, device="cuda")
+        seqs = torch.zeros(ext.slot_blocks(MAXN, 1) + 1, dtype=torch.int64, device="cuda")
+        xs = {r: member_input(30 + r, n) for r in rows}
+        for r in (1, 2):
+            reg.stage(0, r, xs[r], seq=1)
+        out = reduce(ext, reg, 0, o, seqs, xs[0], 1)
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(out), oracle.member_sum([bits(xs[2]), None, bits(xs[0]),
+                                                             bits(xs[1])]))
     finally:
         reg.close()
 
