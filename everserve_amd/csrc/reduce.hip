@@ -37,7 +37,9 @@
 // state[1], whose last adder then writes state[0]. No fence is needed, so no workgroup writes back
 // or invalidates the L2; and no word takes more than ceil(workgroups / G) + G of the atomics,
 // which on MI355X serialise per address at device scope (one word for every workgroup cost
-// 2.8 us of a 13 us call at 256 workgroups). The counting words return to zero at the end of
+// 2.8 us of a 13 us call at 256 workgroups). A grid of at most G workgroups (decode sizes) would
+// put one in each group word, so its workgroups count straight into the top word, and a grid of
+// one counts nothing: it writes state[0] itself. The counting words return to zero at the end of
 // every call, so the launch needs no memset and a captured graph can replay it.
 
 #include "common.hpp"
@@ -306,7 +308,7 @@ __device__ __forceinline__ void finish_call(const ReduceArgs& a,
                                             const uint16_t* const (&src)[kMaxRows], int count,
                                             int64_t nvec, int64_t vb, uint64_t* group_word,
                                             uint64_t group_before, uint32_t group,
-                                            uint32_t groups) {
+                                            uint32_t groups, uint64_t own_outcome) {
   const int tid = threadIdx.x;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads * kVpt;
   // vectors of 8 elements: one 16-byte load per member
@@ -380,14 +382,18 @@ __device__ __forceinline__ void finish_call(const ReduceArgs& a,
   }
 
   if (tid == 0) {
-    const uint32_t in_group = (gridDim.x - group + groups - 1) / groups;  // ids b, b % groups == group
-    uint64_t outcome = 0;
-    if (last(group_word, group_before, in_group, outcome) &&
-        last(a.state + 1, arrive(a.state + 1, outcome), groups, outcome)) {
-      // the last workgroup of the call: every outcome is in `outcome`
+    uint64_t outcome = own_outcome;
+    bool all_in = true;  // this workgroup has every workgroup's outcome in `outcome`
+    if (gridDim.x > kGroups) {
+      const uint32_t in_group = (gridDim.x - group + groups - 1) / groups;  // b % groups == group
+      all_in = last(group_word, group_before, in_group, outcome) &&
+               last(a.state + 1, arrive(a.state + 1, outcome), groups, outcome);
+    } else if (gridDim.x > 1) {
+      all_in = last(group_word, group_before, gridDim.x, outcome);  // group_word is the top word
+    }
+    if (all_in)
       __hip_atomic_store(a.state + 0, (a.epoch << 16) | outcome, __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_SYSTEM);
-    }
   }
 }
 
@@ -451,13 +457,17 @@ __global__ __launch_bounds__(kThreads) void local_reduce(ReduceArgs a) {
   // This workgroup's outcome is settled once its wait is over, so it is counted then: the
   // counting atomic's round trip then overlaps the payload instead of following it. state[0] is
   // read only once the kernel has completed, when every workgroup's payload is written too.
+  // A grid of at most kGroups workgroups would put one in each group word: its workgroups count
+  // straight into the top word, and a grid of one counts nothing (its outcome is the call's).
   const uint32_t groups = gridDim.x < kGroups ? gridDim.x : kGroups;
   const uint32_t group = blockIdx.x % groups;
-  uint64_t* const group_word = a.state + kGroupStride * (1 + group);
+  uint64_t* const group_word =
+      gridDim.x <= kGroups ? a.state + 1 : a.state + kGroupStride * (1 + group);
+  const bool counts = gridDim.x > 1;
   uint64_t group_before = 0;
   const int mode = s_mode;
   const bool waiting = EVS_REDUCE_EARLY && (mode & kEarly) != 0;
-  if (tid == 0 && !waiting) group_before = arrive(group_word, s_outcome);
+  if (tid == 0 && !waiting && counts) group_before = arrive(group_word, s_outcome);
 
   const int count = s_count;
   const int64_t nvec = (mode & kVectors) ? a.nvec : 0;
@@ -495,7 +505,7 @@ __global__ __launch_bounds__(kThreads) void local_reduce(ReduceArgs a) {
       }
     }
     __syncthreads();
-    if (tid == 0) group_before = arrive(group_word, s_outcome);
+    if (tid == 0 && counts) group_before = arrive(group_word, s_outcome);
     load_late(x, s_late, __builtin_amdgcn_readfirstlane(s_came), vb, records, tid);
     sum_store(x, uniform_rsrc(a.out + vb * 8, records), tid);
     vb += static_cast<int64_t>(gridDim.x) * kThreads * kVpt;
@@ -504,12 +514,12 @@ __global__ __launch_bounds__(kThreads) void local_reduce(ReduceArgs a) {
 #pragma unroll
     for (int q = 0; q < kMaxRows; q++)
       if (src[q] == nullptr) src[q] = s_late[q];
-    finish_call(a, src, count, nvec, vb, group_word, group_before, group, groups);
+    finish_call(a, src, count, nvec, vb, group_word, group_before, group, groups, s_outcome);
     return;
   }
 #endif
 
-  finish_call(a, src, count, nvec, vb, group_word, group_before, group, groups);
+  finish_call(a, src, count, nvec, vb, group_word, group_before, group, groups, s_outcome);
 }
 
 int64_t g_clock_khz[64];

@@ -75,7 +75,7 @@ class Members:
         return s >> 16, (s >> 8) & 0xFF, s & 0xFF
 
 
-@pytest.mark.parametrize("n", [16384, 3000, 2, 8 * 256 * 2 + 5])
+@pytest.mark.parametrize("n", [16384, 3000, 2, 8 * 256 * 2 + 5, 40960, 65536])
 @pytest.mark.parametrize("order", [[0, 1, 2], [2, 0, 1], [5, 3, 7, 0, 1, 6, 2, 4]])
 def test_the_sum_is_the_ordered_fp32_sum_bit_for_bit(ext, n, order):
     inputs = {r: bf16_input(1000 * r + n, n) for r in order}
@@ -120,8 +120,10 @@ def test_c5_eight_buffers_of_256_by_8192(ext):
     assert m.status() == (3, 0, 0)
 
 
-def test_a_stalled_flag_ends_in_a_timeout_that_names_it(ext):
-    n = 256 * 8192
+@pytest.mark.parametrize("n", [256 * 8192, 40960, 3000])
+def test_a_stalled_flag_ends_in_a_timeout_that_names_it(ext, n):
+    """At C5 (256 workgroups, counted in two levels), 5 workgroups (counted in the top word) and
+    one (nothing counted): the outcome word names the stalled row each way."""
     order = list(range(8))
     inputs = {r: bf16_input(5 + r, n) for r in order}
     m = Members(inputs, order)
