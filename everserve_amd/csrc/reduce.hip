@@ -59,11 +59,15 @@ constexpr int kMaxRows = EVS_MAX_ROWS;
 #ifndef EVS_REDUCE_VPT
 #define EVS_REDUCE_VPT 4
 #endif
+// At most two workgroups a CU: the 4-vector kernel's registers leave room for two waves a SIMD, so
+// every workgroup of the largest grid is resident at once and each waits out its own bounded wait
+// (a grid past that would time out in turns).
 #ifndef EVS_REDUCE_MAX_BLOCKS
-#define EVS_REDUCE_MAX_BLOCKS 1024
+#define EVS_REDUCE_MAX_BLOCKS 512
 #endif
-constexpr int kVpt = EVS_REDUCE_VPT;  // 8-element vectors per thread per pass
-constexpr int kMaxBlocks = EVS_REDUCE_MAX_BLOCKS;  // all resident on 256 CUs: each polls once
+constexpr int kMaxVpt = EVS_REDUCE_VPT;  // 8-element vectors per thread per pass, at most
+constexpr int kMaxBlocks = EVS_REDUCE_MAX_BLOCKS;  // all resident on 256 CUs
+constexpr int kCUs = 256;          // MI355X's compute units
 constexpr int kPollsPerCheck = 32; // flag polls between clock and ABORT reads
 constexpr int kBadOrder = 4;       // reason bit: `order` named a row outside [0, MAX_ROWS)
 constexpr int kVectors = 1;        // mode bit: every member buffer 16-byte aligned
@@ -237,14 +241,15 @@ __device__ __forceinline__ int pass_records(int64_t nvec, int64_t vb) {
 
 // One pass's payload loads: vector i of every member q, through q's resource (an absent member's
 // resource is empty, so its loads return zeros without touching memory).
-__device__ __forceinline__ void load_pass(u32x4 (&x)[kVpt][kMaxRows],
+template <int V>
+__device__ __forceinline__ void load_pass(u32x4 (&x)[V][kMaxRows],
                                           const __amdgpu_buffer_rsrc_t (&r)[kMaxRows], int tid) {
   // vector-major (1): vector i's loads from every member come before vector i + 1's, so its sum
   // and store can go out while the later vectors' loads are still in flight
 #pragma unroll
-  for (int j = 0; j < kVpt * kMaxRows; j++) {
-    const int i = EVS_REDUCE_LOAD_ORDER ? j / kMaxRows : j % kVpt;
-    const int q = EVS_REDUCE_LOAD_ORDER ? j % kMaxRows : j / kVpt;
+  for (int j = 0; j < V * kMaxRows; j++) {
+    const int i = EVS_REDUCE_LOAD_ORDER ? j / kMaxRows : j % V;
+    const int q = EVS_REDUCE_LOAD_ORDER ? j % kMaxRows : j / V;
     x[i][q] = __builtin_amdgcn_raw_buffer_load_b128(r[q], (i * kThreads + tid) * 16, 0,
                                                     kPayloadScope);
     // keep each vector's loads together, in this order (the scheduler would group them by
@@ -257,7 +262,8 @@ __device__ __forceinline__ void load_pass(u32x4 (&x)[kVpt][kMaxRows],
 // An early start's second round: the vectors of each member q whose bit is set in `late` (the
 // same in every lane), loaded over the zeros the first round read for it. Only those members'
 // loads are issued, into the registers the first round filled, so the round needs none more.
-__device__ __forceinline__ void load_late(u32x4 (&x)[kVpt][kMaxRows],
+template <int V>
+__device__ __forceinline__ void load_late(u32x4 (&x)[V][kMaxRows],
                                           const uint16_t* const (&late_src)[kMaxRows],
                                           uint32_t late, int64_t vb, int records, int tid) {
 #pragma unroll
@@ -265,7 +271,7 @@ __device__ __forceinline__ void load_late(u32x4 (&x)[kVpt][kMaxRows],
     if ((late >> q) & 1) {
       const __amdgpu_buffer_rsrc_t r = uniform_rsrc(late_src[q] + vb * 8, records);
 #pragma unroll
-      for (int i = 0; i < kVpt; i++)
+      for (int i = 0; i < V; i++)
         x[i][q] = __builtin_amdgcn_raw_buffer_load_b128(r, (i * kThreads + tid) * 16, 0,
                                                         kPayloadScope);
     }
@@ -277,10 +283,11 @@ __device__ __forceinline__ void load_late(u32x4 (&x)[kVpt][kMaxRows],
 // through the output resource `ro`, which ends at the last vector, so a store past it is dropped.
 // Adding an absent member's +0.0 changes no sum: the accumulator starts at +0.0 and so is never
 // -0.0. Straight-line, so each vector's sum waits only for its own loads.
-__device__ __forceinline__ void sum_store(const u32x4 (&x)[kVpt][kMaxRows],
+template <int V>
+__device__ __forceinline__ void sum_store(const u32x4 (&x)[V][kMaxRows],
                                           __amdgpu_buffer_rsrc_t ro, int tid) {
 #pragma unroll
-  for (int i = 0; i < kVpt; i++) {
+  for (int i = 0; i < V; i++) {
     float acc[8];
 #pragma unroll
     for (int e = 0; e < 8; e++) acc[e] = 0.0f;
@@ -304,17 +311,18 @@ __device__ __forceinline__ void sum_store(const u32x4 (&x)[kVpt][kMaxRows],
 
 // The rest of a call from vector vb on: the passes of the vector path, the elements the vectors
 // do not cover, and the completion count.
+template <int V>
 __device__ __forceinline__ void finish_call(const ReduceArgs& a,
                                             const uint16_t* const (&src)[kMaxRows], int count,
                                             int64_t nvec, int64_t vb, uint64_t* group_word,
                                             uint64_t group_before, uint32_t group,
                                             uint32_t groups, uint64_t own_outcome) {
   const int tid = threadIdx.x;
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads * kVpt;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads * V;
   // vectors of 8 elements: one 16-byte load per member
   for (; vb < nvec; vb += stride) {
     const int64_t v0 = vb + tid;
-    u32x4 x[kVpt][kMaxRows];
+    u32x4 x[V][kMaxRows];
     if (EVS_REDUCE_FENCE == 3) {
       // a buffer resource per member over this pass's vectors: a load past the end returns 0;
       // an absent member (missing, or past the count) gets an empty resource, so no branch
@@ -329,7 +337,7 @@ __device__ __forceinline__ void finish_call(const ReduceArgs& a,
       continue;
     } else {
 #pragma unroll
-      for (int i = 0; i < kVpt; i++) {
+      for (int i = 0; i < V; i++) {
         const int64_t v = v0 + static_cast<int64_t>(i) * kThreads;
 #pragma unroll
         for (int q = 0; q < kMaxRows; q++) {
@@ -340,7 +348,7 @@ __device__ __forceinline__ void finish_call(const ReduceArgs& a,
       }
     }
 #pragma unroll
-    for (int i = 0; i < kVpt; i++) {
+    for (int i = 0; i < V; i++) {
       const int64_t v = v0 + static_cast<int64_t>(i) * kThreads;
       if (v >= nvec) continue;
       float acc[8];
@@ -397,6 +405,7 @@ __device__ __forceinline__ void finish_call(const ReduceArgs& a,
   }
 }
 
+template <int V>
 __global__ __launch_bounds__(kThreads) void local_reduce(ReduceArgs a) {
   __shared__ const uint16_t* s_src[kMaxRows];  // member in order position q, or null: missing
   __shared__ int s_count;
@@ -404,7 +413,7 @@ __global__ __launch_bounds__(kThreads) void local_reduce(ReduceArgs a) {
   __shared__ uint32_t s_outcome;                 // reason << 8 | late rows
 
   const int tid = threadIdx.x;
-  const int64_t first_vb = static_cast<int64_t>(blockIdx.x) * kThreads * kVpt;  // first vector
+  const int64_t first_vb = static_cast<int64_t>(blockIdx.x) * kThreads * V;  // first vector
   // wave 0's view of the members (lane q: order position q), kept for an early start's wait
   int row = -1, src_lane = 0;
   bool valid = false;
@@ -484,7 +493,7 @@ __global__ __launch_bounds__(kThreads) void local_reduce(ReduceArgs a) {
     // now, and after the wait the members that came in during it. A member that never came in
     // reads as zeros in both. The wait ends on the same events as the one above, so the outcome
     // and the sum equal a wait-then-load call's.
-    u32x4 x[kVpt][kMaxRows];
+    u32x4 x[V][kMaxRows];
     const int records = pass_records(nvec, vb);
     __amdgpu_buffer_rsrc_t r[kMaxRows];
 #pragma unroll
@@ -508,18 +517,18 @@ __global__ __launch_bounds__(kThreads) void local_reduce(ReduceArgs a) {
     if (tid == 0 && counts) group_before = arrive(group_word, s_outcome);
     load_late(x, s_late, __builtin_amdgcn_readfirstlane(s_came), vb, records, tid);
     sum_store(x, uniform_rsrc(a.out + vb * 8, records), tid);
-    vb += static_cast<int64_t>(gridDim.x) * kThreads * kVpt;
+    vb += static_cast<int64_t>(gridDim.x) * kThreads * V;
     // the later passes and the element tail read every member that is in; this path ends here,
     // so the common path's code stays as it is
 #pragma unroll
     for (int q = 0; q < kMaxRows; q++)
       if (src[q] == nullptr) src[q] = s_late[q];
-    finish_call(a, src, count, nvec, vb, group_word, group_before, group, groups, s_outcome);
+    finish_call<V>(a, src, count, nvec, vb, group_word, group_before, group, groups, s_outcome);
     return;
   }
 #endif
 
-  finish_call(a, src, count, nvec, vb, group_word, group_before, group, groups, s_outcome);
+  finish_call<V>(a, src, count, nvec, vb, group_word, group_before, group, groups, s_outcome);
 }
 
 int64_t g_clock_khz[64];
@@ -573,14 +582,33 @@ extern "C" int evs_local_reduce(const int64_t* bufs, const uint64_t* flags, cons
   a.max_polls = static_cast<uint64_t>(timeout_ns / 50) + 4096;
   a.ctrl = ctrl;
   a.state = state;
-  const int64_t per_block = static_cast<int64_t>(evs::kThreads) * evs::kVpt;
+  // Vectors per thread: the fewest (1, 2, then kMaxVpt) that keep the grid within one workgroup
+  // a CU. A thread's loads of one vector from every member go out together; more vectors a
+  // thread than the data needs only add loads that read nothing, and fewer, fatter workgroups
+  // than CUs leave CUs idle (measured on MI355X: 1 vector a thread is fastest up to 512 Ki
+  // elements, 2 at 1 Mi, 4 at 2 Mi).
+  int vpt = evs::kMaxVpt;
+  for (const int v : {1, 2}) {
+    if (v < vpt && (a.nvec + int64_t{evs::kThreads} * v - 1) / (int64_t{evs::kThreads} * v) <=
+                       evs::kCUs) {
+      vpt = v;
+      break;
+    }
+  }
+  const int64_t per_block = static_cast<int64_t>(evs::kThreads) * vpt;
   int64_t blocks = (a.nvec + per_block - 1) / per_block;
   const int64_t tail_blocks = (n - a.nvec * 8 + evs::kThreads - 1) / evs::kThreads;
   if (tail_blocks > blocks) blocks = tail_blocks;
   if (blocks < 1) blocks = 1;
   if (blocks > evs::kMaxBlocks) blocks = evs::kMaxBlocks;
-  hipLaunchKernelGGL(evs::local_reduce, dim3(static_cast<uint32_t>(blocks)), dim3(evs::kThreads),
-                     0, evs::as_stream(stream), a);
+  const dim3 grid(static_cast<uint32_t>(blocks)), block(evs::kThreads);
+  hipStream_t s = evs::as_stream(stream);
+  if (vpt == 1)
+    hipLaunchKernelGGL(evs::local_reduce<1>, grid, block, 0, s, a);
+  else if (vpt == 2)
+    hipLaunchKernelGGL(evs::local_reduce<2>, grid, block, 0, s, a);
+  else
+    hipLaunchKernelGGL(evs::local_reduce<evs::kMaxVpt>, grid, block, 0, s, a);
   EVS_LAUNCHED("evs_local_reduce");
   return EVS_OK;
 }

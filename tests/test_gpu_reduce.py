@@ -120,10 +120,11 @@ def test_c5_eight_buffers_of_256_by_8192(ext):
     assert m.status() == (3, 0, 0)
 
 
-@pytest.mark.parametrize("n", [256 * 8192, 40960, 3000])
+@pytest.mark.parametrize("n", [256 * 8192, 40960, 10000, 2048])
 def test_a_stalled_flag_ends_in_a_timeout_that_names_it(ext, n):
-    """At C5 (256 workgroups, counted in two levels), 5 workgroups (counted in the top word) and
-    one (nothing counted): the outcome word names the stalled row each way."""
+    """At C5 (256 workgroups of 4 vectors a thread), 40960 elements (20 workgroups of 1: both
+    counted in two levels), 10000 (5 workgroups, counted in the top word) and 2048 (one, nothing
+    counted): the outcome word names the stalled row each way."""
     order = list(range(8))
     inputs = {r: bf16_input(5 + r, n) for r in order}
     m = Members(inputs, order)
