@@ -44,9 +44,10 @@ constexpr int kSlotThreads = 256;
 constexpr int kMaxRows = EVS_MAX_ROWS;
 constexpr uint32_t kCheckEvery = 1024;
 
-// Members whose words a thread waits on together: every member at up to 8 words a thread (at most
-// 128 VGPRs of words), 4 at 16. One round of loads then covers a whole batch, so a call of k <= 8
-// members at decode sizes waits for one round trip, not one a batch.
+// Members whose words a thread waits on together: every member (up to 8) at 1 or 2 words a
+// thread, 4 at more, where 8 members' words would hold 64-256 VGPRs. One round of loads then
+// covers a whole batch, so a call of k <= 8 members at 1 word a thread (the driver's setting)
+// waits for one round trip a poll, not one a batch.
 template <int W>
 constexpr int batch_of() {
   return W <= 2 ? kMaxRows : 4;
