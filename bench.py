@@ -1137,12 +1137,32 @@ def bench_decode_overhead(ext, steps, warmup):
 
     graph8, out8 = capture(forward8)
 
+    # the same fp8 step at batch 32 (the first 32 sequences, their K and V), a step that fits in
+    # 5 ms on MI355X: the snapshot's share of a shorter step
+    B32 = 32
+    x32 = x0[:B32].contiguous()
+
+    def forward8_b32():
+        x = x32
+        for p, p8 in zip(w, w8):
+            qkv = lin8(x, p8["qkv"])
+            q = qkv[:, : HQ * DH].reshape(B32 * HKV, 1, HQ // HKV, DH)
+            a = F.scaled_dot_product_attention(q, p["k"][: B32 * HKV], p["v"][: B32 * HKV])
+            x = x + lin8(a.reshape(B32, HQ * DH), p8["o"])
+            gu = lin8(x, p8["up"])
+            x = x + lin8(F.silu(gu[:, :FF]) * gu[:, FF:], p8["down"])
+        return x
+
+    graph8_32, out8_32 = capture(forward8_b32)
+
     # the snapshot: the step's 64 new slots, every layer and head, into a staging file
     from everserve_amd.state.staging import StepStager
 
     NB, BS = 4096, 16
     cache = [torch.randn(2, NB, BS, HKV, DH, device=dev, dtype=bf) for _ in range(Lyr)]
     kv = {f"model.layers.{i}.self_attn.attn": t for i, t in enumerate(cache)}
+    slot_sets_32 = [torch.arange(i * B32, (i + 1) * B32, dtype=torch.long, device=dev) * 7
+                    % (NB * BS) for i in range(4)]
     slot_sets = [torch.arange(i * B, (i + 1) * B, dtype=torch.long, device=dev) * 7 % (NB * BS)
                  for i in range(4)]
     staged = {"steps": 0}
@@ -1162,11 +1182,12 @@ def bench_decode_overhead(ext, steps, warmup):
     step_no = [0]
 
     def step(mode: str, i: int):
-        g, o = (graph8, out8) if mode.endswith("_fp8") else (graph, out)
+        g, o = ((graph8_32, out8_32) if mode.endswith("_fp8_b32")
+                else (graph8, out8) if mode.endswith("_fp8") else (graph, out))
         g.replay()
         if mode.startswith("stager"):
             step_no[0] += 1
-            sl = slot_sets[i % 4]
+            sl = (slot_sets_32 if mode.endswith("_b32") else slot_sets)[i % 4]
             for name, t in kv.items():
                 stager.save(name, t, sl)
             stager.commit(0, step_no[0], {})
@@ -1189,7 +1210,8 @@ def bench_decode_overhead(ext, steps, warmup):
         torch.cuda.synchronize()
         return (time.perf_counter() - t0) / k
 
-    modes = ("none", "stager", "side_stream", "none_fp8", "stager_fp8")
+    modes = ("none", "stager", "side_stream", "none_fp8", "stager_fp8", "none_fp8_b32",
+             "stager_fp8_b32")
     for _ in range(max(2, warmup)):
         for m in modes:
             step(m, 0)
@@ -1206,9 +1228,12 @@ def bench_decode_overhead(ext, steps, warmup):
     best = {m: min(v) for m, v in times.items()}
     off, on = best["none"], best["stager"]
     off8, on8 = best["none_fp8"], best["stager_fp8"]
+    off32, on32 = best["none_fp8_b32"], best["stager_fp8_b32"]
     # the step as it would run at 75 % of HBM peak: the time the proxy's bytes take there
     roof_s = step_bytes / (0.75 * PEAK_HBM_GBS * 1e9)
-    del w, w8, cache, graph, graph8
+    # the batch-32 step reads half the K and V
+    step8_32_bytes = step8_bytes - Lyr * (B - B32) * HKV * CTX * DH * 2 * 2
+    del w, w8, cache, graph, graph8, graph8_32
     torch.cuda.empty_cache()
     return {
         "config": "Llama-3-8B decode-step proxy: 32 layers, batch 64, ctx 1024, bf16 (nn.Linear "
@@ -1241,6 +1266,15 @@ def bench_decode_overhead(ext, steps, warmup):
             "added_percent": round((on8 - off8) / off8 * 100, 3),
             "proxy_bytes_per_step": step8_bytes,
             "proxy_hbm_gbs": round(step8_bytes / off8 / 1e9, 1),
+        },
+        "fp8_weights_batch32": {
+            "how": "the fp8 step over the first 32 sequences; snapshot = their 32 slots (4 MiB)",
+            "step_ms_without": round(off32 * 1e3, 4),
+            "step_ms_with": round(on32 * 1e3, 4),
+            "added_us_per_step": round((on32 - off32) * 1e6, 2),
+            "added_percent": round((on32 - off32) / off32 * 100, 3),
+            "proxy_bytes_per_step": step8_32_bytes,
+            "proxy_hbm_gbs": round(step8_32_bytes / off32 / 1e9, 1),
         },
         "rounds_ms": {m: [round(x * 1e3, 4) for x in v] for m, v in times.items()},
     }
