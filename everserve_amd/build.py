@@ -33,6 +33,11 @@ SOURCES = ("rows.hip", "order.hip", "reduce.hip", "slot.hip", "host_rows.hip", "
 HEADERS = ("common.hpp", "host_copy.hpp", "workers.hpp")
 PUBLIC_HEADERS = ("everserve_mi355x.h",)
 DEFAULT_ARCHS = "gfx950"
+# Flags for one source only. The local reduce's counting atomics run in one lane and their
+# answers are read late; the atomic optimizer would rewrite each into a wave-wide form that reads
+# its answer at once (to hand it to every lane), which waits out the atomic in front of the
+# payload loads.
+SOURCE_FLAGS = {"reduce.hip": ("-mllvm", "-amdgpu-atomic-optimizer-strategy=None")}
 
 HIPCC_FLAGS = [
     "-O3",
@@ -62,11 +67,12 @@ def source_files() -> list[Path]:
 
 
 def sources_digest() -> str:
-    """sha256 over the names and bytes of every source file."""
+    """sha256 over the names and bytes of every source file, and the flags they are built with."""
     digest = hashlib.sha256()
     for f in source_files():
         digest.update(f.name.encode())
         digest.update(f.read_bytes())
+    digest.update(json.dumps([HIPCC_FLAGS, SOURCE_FLAGS], sort_keys=True).encode())
     return digest.hexdigest()
 
 
@@ -97,8 +103,8 @@ def build(out_dir: Path = PACKAGE, archs: str | None = None, verbose: bool = Fal
 
     def compile_one(src: str) -> Path:
         obj = obj_dir / (Path(src).stem + ".o")
-        cmd = [cc, *HIPCC_FLAGS, *arch_flags, *includes, *[f"-D{d}" for d in defines], "-c",
-               str(CSRC / src), "-o", str(obj)]
+        cmd = [cc, *HIPCC_FLAGS, *SOURCE_FLAGS.get(src, ()), *arch_flags, *includes,
+               *[f"-D{d}" for d in defines], "-c", str(CSRC / src), "-o", str(obj)]
         if verbose:
             print(" ".join(cmd), flush=True)
         subprocess.run(cmd, check=True, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)

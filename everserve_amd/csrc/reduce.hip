@@ -40,7 +40,10 @@
 // 2.8 us of a 13 us call at 256 workgroups). A grid of at most G workgroups (decode sizes) would
 // put one in each group word, so its workgroups count straight into the top word, and a grid of
 // one counts nothing: it writes state[0] itself. The counting words return to zero at the end of
-// every call, so the launch needs no memset and a captured graph can replay it.
+// every call, so the launch needs no memset and a captured graph can replay it. These atomics run
+// in one lane and their answers are read late; the file is built without the compiler's atomic
+// optimizer, whose wave-wide form of them would read each answer at once and so wait out the
+// round trip in front of the payload loads.
 
 #include "common.hpp"
 
@@ -319,6 +322,13 @@ __device__ __forceinline__ void finish_call(const ReduceArgs& a,
                                             uint32_t groups, uint64_t own_outcome) {
   const int tid = threadIdx.x;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads * V;
+  // Two-level counting: the group's last workgroup carries the group's outcome to the top word.
+  // It does so right after its first pass's loads are issued: its wait for the group word's
+  // answer (counted before the payload) then leaves those loads in flight, and the top word's
+  // answer is only read at the end, so no atomic round trip is left for the end of the call.
+  const bool two_level = gridDim.x > kGroups;
+  bool top_sent = false, group_last = false;
+  uint64_t group_all = 0, top_before = 0;
   // vectors of 8 elements: one 16-byte load per member
   for (; vb < nvec; vb += stride) {
     const int64_t v0 = vb + tid;
@@ -333,6 +343,14 @@ __device__ __forceinline__ void finish_call(const ReduceArgs& a,
       for (int q = 0; q < kMaxRows; q++)
         r[q] = src[q] != nullptr ? uniform_rsrc(src[q] + vb * 8, records) : uniform_rsrc(a.out, 0);
       load_pass(x, r, tid);
+      if (two_level && tid == 0 && !top_sent) {
+        // the group word's answer is read here, behind this pass's loads, not before the loop
+        asm volatile("" : "+v"(group_before));
+        top_sent = true;
+        const uint32_t in_group = (gridDim.x - group + groups - 1) / groups;  // b % groups == group
+        group_last = last(group_word, group_before, in_group, group_all);
+        if (group_last) top_before = arrive(a.state + 1, group_all);
+      }
       sum_store(x, uniform_rsrc(a.out + vb * 8, records), tid);
       continue;
     } else {
@@ -392,10 +410,13 @@ __device__ __forceinline__ void finish_call(const ReduceArgs& a,
   if (tid == 0) {
     uint64_t outcome = own_outcome;
     bool all_in = true;  // this workgroup has every workgroup's outcome in `outcome`
-    if (gridDim.x > kGroups) {
-      const uint32_t in_group = (gridDim.x - group + groups - 1) / groups;  // b % groups == group
-      all_in = last(group_word, group_before, in_group, outcome) &&
-               last(a.state + 1, arrive(a.state + 1, outcome), groups, outcome);
+    if (two_level) {
+      if (!top_sent) {  // no vector pass ran here: carry the group's outcome now
+        const uint32_t in_group = (gridDim.x - group + groups - 1) / groups;
+        group_last = last(group_word, group_before, in_group, group_all);
+        if (group_last) top_before = arrive(a.state + 1, group_all);
+      }
+      all_in = group_last && last(a.state + 1, top_before, groups, outcome);
     } else if (gridDim.x > 1) {
       all_in = last(group_word, group_before, gridDim.x, outcome);  // group_word is the top word
     }
