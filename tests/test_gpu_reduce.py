@@ -228,6 +228,40 @@ def test_members_that_arrive_late_in_the_middle_of_the_order(ext, n):
         ext.host_free(flags_host)
 
 
+@pytest.mark.parametrize("n", [256 * 256 * 8, 256 * 256 * 8 + 13, 2 * 256 * 256 * 8,
+                               2 * 256 * 256 * 8 + 8 * 5 + 3])
+def test_grids_at_the_vector_width_thresholds(ext, n):
+    """The launch takes 1, 2 or 4 vectors a thread, the fewest that keep the grid within 256
+    workgroups: these sizes sit on either side of the 1 -> 2 and 2 -> 4 switches. At each, every
+    member in, then one of them arriving while the call waits, summed as the oracle does."""
+    flags_host, flags_dev = ext.host_alloc_mapped(MAXW * 8)
+    try:
+        words = (ctypes.c_int64 * MAXW).from_address(flags_host)
+        order = [6, 1, 4, 0, 7, 2, 5, 3]
+        inputs = {r: bf16_input(200 + r, n) for r in order}
+        m = Members(inputs, order)
+        want = oracle.member_sum([bits(inputs[r]) for r in order])
+        for r in order:
+            words[r] = 1
+        ext.local_reduce(m.bufs, flags_dev, m.order, m.out, 1, 3_000_000_000, 0, m.state)
+        torch.cuda.synchronize()
+        assert m.status() == (1, 0, 0)
+        assert np.array_equal(bits(m.out), want)
+        m.out.zero_()
+        for r in order:
+            words[r] = 0 if r == 0 else 2
+        torch.cuda.synchronize()
+        ext.local_reduce(m.bufs, flags_dev, m.order, m.out, 2, 3_000_000_000, 0, m.state)
+        time.sleep(0.01)
+        words[0] = 2
+        torch.cuda.synchronize()
+        assert m.status() == (2, 0, 0)
+        assert np.array_equal(bits(m.out), want)
+        assert not m.state[1:].any()
+    finally:
+        ext.host_free(flags_host)
+
+
 def test_a_late_member_that_never_comes_reads_as_zeros_mid_order(ext):
     """A member missing at the first read and never arriving: the members loaded before the wait
     are summed with zeros in its place, and the timeout names it."""
