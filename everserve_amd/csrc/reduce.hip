@@ -37,9 +37,12 @@
 // state[1], whose last adder then writes state[0]. No fence is needed, so no workgroup writes back
 // or invalidates the L2; and no word takes more than ceil(workgroups / G) + G of the atomics,
 // which on MI355X serialise per address at device scope (one word for every workgroup cost
-// 2.8 us of a 13 us call at 256 workgroups). A grid of at most G workgroups (decode sizes) would
-// put one in each group word, so its workgroups count straight into the top word, and a grid of
-// one counts nothing: it writes state[0] itself. The counting words return to zero at the end of
+// 2.8 us of a 13 us call at 256 workgroups). A grid of at most EVS_REDUCE_FLAT_MAX workgroups
+// (decode sizes) counts straight into the top word instead, and a grid of one counts nothing: it
+// writes state[0] itself. The counting mode is a template parameter chosen at launch, so each
+// kernel holds only its own mode's code: on MI355X the code of modes a call does not run cost a
+// small grid 0.2-0.3 us, through the registers and schedule of its payload loop. The counting
+// words return to zero at the end of
 // every call, so the launch needs no memset and a captured graph can replay it. These atomics run
 // in one lane and their answers are read late; the file is built without the compiler's atomic
 // optimizer, whose wave-wide form of them would read each answer at once and so wait out the
@@ -77,6 +80,20 @@ constexpr int kVectors = 1;        // mode bit: every member buffer 16-byte alig
 constexpr int kEarly = 2;          // mode bit: early start (a member missing at the first read)
 constexpr int kDoneBits = 20;      // counting words: workgroups done in bits [0, 20), outcome above
 constexpr uint32_t kGroups = 8;    // group counting words
+// Grids up to this many workgroups count flat, into the top word: their atomics on one address
+// cost less than the second level's round trip. Measured on MI355X, k = 8: at 32 workgroups flat
+// ran 3.28 us against 3.54 for two levels; at 64 the two were within the spread between runs;
+// at 128 flat ran 4.26 us against 3.48-3.62.
+#ifndef EVS_REDUCE_FLAT_MAX
+#define EVS_REDUCE_FLAT_MAX 32
+#endif
+constexpr uint32_t kFlatMax = EVS_REDUCE_FLAT_MAX;
+static_assert(kFlatMax >= kGroups && kFlatMax < (1u << 20), "flat counting bound");
+// counting modes (a kernel template parameter): a grid of one counts nothing; a grid of at most
+// kFlatMax counts in the top word; any grid may count in two levels
+constexpr int kCountNone = 0;
+constexpr int kCountFlat = 1;
+constexpr int kCountTwoLevel = 2;
 constexpr int kGroupStride = 32;   // words between counting words (256 bytes)
 static_assert(kGroupStride * (1 + kGroups) <= EVS_REDUCE_STATE_WORDS, "state record too small");
 
@@ -313,8 +330,8 @@ __device__ __forceinline__ void sum_store(const u32x4 (&x)[V][kMaxRows],
 }
 
 // The rest of a call from vector vb on: the passes of the vector path, the elements the vectors
-// do not cover, and the completion count.
-template <int V>
+// do not cover, and the completion count (in counting mode C).
+template <int V, int C>
 __device__ __forceinline__ void finish_call(const ReduceArgs& a,
                                             const uint16_t* const (&src)[kMaxRows], int count,
                                             int64_t nvec, int64_t vb, uint64_t* group_word,
@@ -326,7 +343,7 @@ __device__ __forceinline__ void finish_call(const ReduceArgs& a,
   // It does so right after its first pass's loads are issued: its wait for the group word's
   // answer (counted before the payload) then leaves those loads in flight, and the top word's
   // answer is only read at the end, so no atomic round trip is left for the end of the call.
-  const bool two_level = gridDim.x > kGroups;
+  constexpr bool two_level = C == kCountTwoLevel;
   bool top_sent = false, group_last = false;
   uint64_t group_all = 0, top_before = 0;
   // vectors of 8 elements: one 16-byte load per member
@@ -417,7 +434,7 @@ __device__ __forceinline__ void finish_call(const ReduceArgs& a,
         if (group_last) top_before = arrive(a.state + 1, group_all);
       }
       all_in = group_last && last(a.state + 1, top_before, groups, outcome);
-    } else if (gridDim.x > 1) {
+    } else if (C == kCountFlat) {
       all_in = last(group_word, group_before, gridDim.x, outcome);  // group_word is the top word
     }
     if (all_in)
@@ -426,7 +443,7 @@ __device__ __forceinline__ void finish_call(const ReduceArgs& a,
   }
 }
 
-template <int V>
+template <int V, int C>
 __global__ __launch_bounds__(kThreads) void local_reduce(ReduceArgs a) {
   __shared__ const uint16_t* s_src[kMaxRows];  // member in order position q, or null: missing
   __shared__ int s_count;
@@ -487,13 +504,13 @@ __global__ __launch_bounds__(kThreads) void local_reduce(ReduceArgs a) {
   // This workgroup's outcome is settled once its wait is over, so it is counted then: the
   // counting atomic's round trip then overlaps the payload instead of following it. state[0] is
   // read only once the kernel has completed, when every workgroup's payload is written too.
-  // A grid of at most kGroups workgroups would put one in each group word: its workgroups count
-  // straight into the top word, and a grid of one counts nothing (its outcome is the call's).
+  // Flat counting puts every workgroup in the top word; a grid of one counts nothing (its outcome
+  // is the call's).
   const uint32_t groups = gridDim.x < kGroups ? gridDim.x : kGroups;
   const uint32_t group = blockIdx.x % groups;
   uint64_t* const group_word =
-      gridDim.x <= kGroups ? a.state + 1 : a.state + kGroupStride * (1 + group);
-  const bool counts = gridDim.x > 1;
+      C == kCountTwoLevel ? a.state + kGroupStride * (1 + group) : a.state + 1;
+  constexpr bool counts = C != kCountNone;
   uint64_t group_before = 0;
   const int mode = s_mode;
   const bool waiting = EVS_REDUCE_EARLY && (mode & kEarly) != 0;
@@ -544,12 +561,13 @@ __global__ __launch_bounds__(kThreads) void local_reduce(ReduceArgs a) {
 #pragma unroll
     for (int q = 0; q < kMaxRows; q++)
       if (src[q] == nullptr) src[q] = s_late[q];
-    finish_call<V>(a, src, count, nvec, vb, group_word, group_before, group, groups, s_outcome);
+    finish_call<V, C>(a, src, count, nvec, vb, group_word, group_before, group, groups,
+                      s_outcome);
     return;
   }
 #endif
 
-  finish_call<V>(a, src, count, nvec, vb, group_word, group_before, group, groups, s_outcome);
+  finish_call<V, C>(a, src, count, nvec, vb, group_word, group_before, group, groups, s_outcome);
 }
 
 int64_t g_clock_khz[64];
@@ -624,12 +642,19 @@ extern "C" int evs_local_reduce(const int64_t* bufs, const uint64_t* flags, cons
   if (blocks > evs::kMaxBlocks) blocks = evs::kMaxBlocks;
   const dim3 grid(static_cast<uint32_t>(blocks)), block(evs::kThreads);
   hipStream_t s = evs::as_stream(stream);
-  if (vpt == 1)
-    hipLaunchKernelGGL(evs::local_reduce<1>, grid, block, 0, s, a);
+  // The counting mode follows the grid. Two-level counting is right for any grid, so the wider
+  // kernels, whose grids are past the flat bound whenever the rule above picks them, carry only it.
+  if (vpt == 1 && blocks == 1)
+    hipLaunchKernelGGL((evs::local_reduce<1, evs::kCountNone>), grid, block, 0, s, a);
+  else if (vpt == 1 && blocks <= evs::kFlatMax)
+    hipLaunchKernelGGL((evs::local_reduce<1, evs::kCountFlat>), grid, block, 0, s, a);
+  else if (vpt == 1)
+    hipLaunchKernelGGL((evs::local_reduce<1, evs::kCountTwoLevel>), grid, block, 0, s, a);
   else if (vpt == 2)
-    hipLaunchKernelGGL(evs::local_reduce<2>, grid, block, 0, s, a);
+    hipLaunchKernelGGL((evs::local_reduce<2, evs::kCountTwoLevel>), grid, block, 0, s, a);
   else
-    hipLaunchKernelGGL(evs::local_reduce<evs::kMaxVpt>, grid, block, 0, s, a);
+    hipLaunchKernelGGL((evs::local_reduce<evs::kMaxVpt, evs::kCountTwoLevel>), grid, block, 0, s,
+                       a);
   EVS_LAUNCHED("evs_local_reduce");
   return EVS_OK;
 }

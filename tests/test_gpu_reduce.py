@@ -120,11 +120,11 @@ def test_c5_eight_buffers_of_256_by_8192(ext):
     assert m.status() == (3, 0, 0)
 
 
-@pytest.mark.parametrize("n", [256 * 8192, 40960, 10000, 2048])
+@pytest.mark.parametrize("n", [256 * 8192, 81920, 65536, 10000, 2048])
 def test_a_stalled_flag_ends_in_a_timeout_that_names_it(ext, n):
-    """At C5 (256 workgroups of 4 vectors a thread), 40960 elements (20 workgroups of 1: both
-    counted in two levels), 10000 (5 workgroups, counted in the top word) and 2048 (one, nothing
-    counted): the outcome word names the stalled row each way."""
+    """At C5 (256 workgroups of 4 vectors a thread) and 81920 elements (40 workgroups of 1), both
+    counted in two levels; 65536 (32 workgroups) and 10000 (5), counted in the top word; and 2048
+    (one, nothing counted): the outcome word names the stalled row each way."""
     order = list(range(8))
     inputs = {r: bf16_input(5 + r, n) for r in order}
     m = Members(inputs, order)
@@ -228,12 +228,16 @@ def test_members_that_arrive_late_in_the_middle_of_the_order(ext, n):
         ext.host_free(flags_host)
 
 
-@pytest.mark.parametrize("n", [256 * 256 * 8, 256 * 256 * 8 + 13, 2 * 256 * 256 * 8,
+@pytest.mark.parametrize("n", [2048, 2048 + 8, 32 * 256 * 8, 32 * 256 * 8 + 8,
+                               256 * 256 * 8, 256 * 256 * 8 + 13, 2 * 256 * 256 * 8,
                                2 * 256 * 256 * 8 + 8 * 5 + 3])
-def test_grids_at_the_vector_width_thresholds(ext, n):
+def test_grids_at_the_launch_thresholds(ext, n):
     """The launch takes 1, 2 or 4 vectors a thread, the fewest that keep the grid within 256
-    workgroups: these sizes sit on either side of the 1 -> 2 and 2 -> 4 switches. At each, every
-    member in, then one of them arriving while the call waits, summed as the oracle does."""
+    workgroups, and counts completion by the grid: not at all in a grid of one, in the top word
+    up to 32 workgroups, in two levels past that. These sizes sit on either side of each switch:
+    1 | 2 and 32 | 33 workgroups of 1 vector a thread, then the 1 -> 2 and 2 -> 4 vector
+    switches. At each, every member in, then one of them arriving while the call waits, summed as
+    the oracle does, with the counting words back at zero."""
     flags_host, flags_dev = ext.host_alloc_mapped(MAXW * 8)
     try:
         words = (ctypes.c_int64 * MAXW).from_address(flags_host)
