@@ -115,6 +115,11 @@ static_assert(kGroupStride * (1 + kGroups) <= EVS_REDUCE_STATE_WORDS, "state rec
 #ifndef EVS_REDUCE_EARLY
 #define EVS_REDUCE_EARLY 1
 #endif
+// Only the kernels of at least this many vectors a thread start early: their first pass is worth
+// issuing before the wait. The others wait first, and carry no early-start code.
+#ifndef EVS_REDUCE_EARLY_MIN_VPT
+#define EVS_REDUCE_EARLY_MIN_VPT 2
+#endif
 #if EVS_REDUCE_EARLY && EVS_REDUCE_FENCE != 3
 #error "early start needs the coherent buffer loads (EVS_REDUCE_FENCE 3)"
 #endif
@@ -445,6 +450,7 @@ __device__ __forceinline__ void finish_call(const ReduceArgs& a,
 
 template <int V, int C>
 __global__ __launch_bounds__(kThreads) void local_reduce(ReduceArgs a) {
+  constexpr bool kStartsEarly = EVS_REDUCE_EARLY && V >= EVS_REDUCE_EARLY_MIN_VPT;
   __shared__ const uint16_t* s_src[kMaxRows];  // member in order position q, or null: missing
   __shared__ int s_count;
   __shared__ int s_mode;                         // kVectors | kEarly
@@ -483,7 +489,7 @@ __global__ __launch_bounds__(kThreads) void local_reduce(ReduceArgs a) {
     const bool unaligned = __ballot((addr & 15) != 0) != 0;
     // Early start: with a member missing, every wave loads this workgroup's first pass of the
     // members already in, and this wave waits for the rest after issuing its share.
-    const bool early = EVS_REDUCE_EARLY && missing != 0 && !unaligned && first_vb < a.nvec;
+    const bool early = kStartsEarly && missing != 0 && !unaligned && first_vb < a.nvec;
     uint32_t late_rows = 0;
     if (missing != 0 && !early)
       missing = wait_members(a, lane, valid, src_lane, row, missing, reason, late_rows);
@@ -513,7 +519,7 @@ __global__ __launch_bounds__(kThreads) void local_reduce(ReduceArgs a) {
   constexpr bool counts = C != kCountNone;
   uint64_t group_before = 0;
   const int mode = s_mode;
-  const bool waiting = EVS_REDUCE_EARLY && (mode & kEarly) != 0;
+  const bool waiting = kStartsEarly && (mode & kEarly) != 0;
   if (tid == 0 && !waiting && counts) group_before = arrive(group_word, s_outcome);
 
   const int count = s_count;
@@ -523,47 +529,49 @@ __global__ __launch_bounds__(kThreads) void local_reduce(ReduceArgs a) {
 #pragma unroll
   for (int q = 0; q < kMaxRows; q++) src[q] = q < count ? s_src[q] : nullptr;
 #if EVS_REDUCE_EARLY
-  __shared__ const uint16_t* s_late[kMaxRows];  // member q if it came in during the wait
-  __shared__ uint32_t s_came;                     // the order positions s_late names
-  // unlikely: the call whose members are all in at the first read does not run this
-  if (__builtin_expect(waiting, 0)) {
-    // The first pass in two rounds of loads: the members that were in at the first read, issued
-    // now, and after the wait the members that came in during it. A member that never came in
-    // reads as zeros in both. The wait ends on the same events as the one above, so the outcome
-    // and the sum equal a wait-then-load call's.
-    u32x4 x[V][kMaxRows];
-    const int records = pass_records(nvec, vb);
-    __amdgpu_buffer_rsrc_t r[kMaxRows];
+  if constexpr (kStartsEarly) {
+    __shared__ const uint16_t* s_late[kMaxRows];  // member q if it came in during the wait
+    __shared__ uint32_t s_came;                     // the order positions s_late names
+    // unlikely: the call whose members are all in at the first read does not run this
+    if (__builtin_expect(waiting, 0)) {
+      // The first pass in two rounds of loads: the members that were in at the first read, issued
+      // now, and after the wait the members that came in during it. A member that never came in
+      // reads as zeros in both. The wait ends on the same events as the one above, so the outcome
+      // and the sum equal a wait-then-load call's.
+      u32x4 x[V][kMaxRows];
+      const int records = pass_records(nvec, vb);
+      __amdgpu_buffer_rsrc_t r[kMaxRows];
 #pragma unroll
-    for (int q = 0; q < kMaxRows; q++)
-      r[q] = src[q] != nullptr ? uniform_rsrc(src[q] + vb * 8, records) : uniform_rsrc(a.out, 0);
-    load_pass(x, r, tid);
-    if (tid < 64) {
-      const int lane = tid;
-      uint32_t late_rows = 0;
-      const uint64_t still = wait_members(a, lane, valid && ((missing >> lane) & 1), src_lane,
-                                          row, missing, reason, late_rows);
-      const uint64_t came = missing & ~still;  // positions that came in during the wait
-      if (lane < kMaxRows)
-        s_late[lane] = (came >> lane) & 1 ? reinterpret_cast<const uint16_t*>(addr) : nullptr;
-      if (lane == 0) {
-        s_came = static_cast<uint32_t>(came);
-        s_outcome = (reason << 8) | late_rows;
+      for (int q = 0; q < kMaxRows; q++)
+        r[q] = src[q] != nullptr ? uniform_rsrc(src[q] + vb * 8, records) : uniform_rsrc(a.out, 0);
+      load_pass(x, r, tid);
+      if (tid < 64) {
+        const int lane = tid;
+        uint32_t late_rows = 0;
+        const uint64_t still = wait_members(a, lane, valid && ((missing >> lane) & 1), src_lane,
+                                            row, missing, reason, late_rows);
+        const uint64_t came = missing & ~still;  // positions that came in during the wait
+        if (lane < kMaxRows)
+          s_late[lane] = (came >> lane) & 1 ? reinterpret_cast<const uint16_t*>(addr) : nullptr;
+        if (lane == 0) {
+          s_came = static_cast<uint32_t>(came);
+          s_outcome = (reason << 8) | late_rows;
+        }
       }
-    }
-    __syncthreads();
-    if (tid == 0 && counts) group_before = arrive(group_word, s_outcome);
-    load_late(x, s_late, __builtin_amdgcn_readfirstlane(s_came), vb, records, tid);
-    sum_store(x, uniform_rsrc(a.out + vb * 8, records), tid);
-    vb += static_cast<int64_t>(gridDim.x) * kThreads * V;
-    // the later passes and the element tail read every member that is in; this path ends here,
-    // so the common path's code stays as it is
+      __syncthreads();
+      if (tid == 0 && counts) group_before = arrive(group_word, s_outcome);
+      load_late(x, s_late, __builtin_amdgcn_readfirstlane(s_came), vb, records, tid);
+      sum_store(x, uniform_rsrc(a.out + vb * 8, records), tid);
+      vb += static_cast<int64_t>(gridDim.x) * kThreads * V;
+      // the later passes and the element tail read every member that is in; this path ends here,
+      // so the common path's code stays as it is
 #pragma unroll
-    for (int q = 0; q < kMaxRows; q++)
-      if (src[q] == nullptr) src[q] = s_late[q];
-    finish_call<V, C>(a, src, count, nvec, vb, group_word, group_before, group, groups,
-                      s_outcome);
-    return;
+      for (int q = 0; q < kMaxRows; q++)
+        if (src[q] == nullptr) src[q] = s_late[q];
+      finish_call<V, C>(a, src, count, nvec, vb, group_word, group_before, group, groups,
+                        s_outcome);
+      return;
+    }
   }
 #endif
 
