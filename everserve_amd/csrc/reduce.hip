@@ -24,7 +24,9 @@
 // only the members that came in during it, into the registers that read zeros for them. Every
 // load still follows the observation of its member's flag, and the sum still runs in the member
 // order, so the result and the outcome equal those of waiting first. After a late flag, the call
-// then has only the late members' loads left instead of every member's.
+// then has only the late members' loads left instead of every member's. Only the kernels of 2 and
+// 4 vectors a thread start early: at 1 a workgroup's first pass is too small to gain from it, and
+// the unrun path's code slowed the all-in call.
 //
 // The call's outcome is one word, state[0] = (epoch << 16) | (reason << 8) | late rows, written by
 // the last workgroup to count. Each workgroup counts once its wait is over, before its payload:
