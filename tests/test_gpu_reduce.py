@@ -284,10 +284,13 @@ def test_a_late_member_that_never_comes_reads_as_zeros_mid_order(ext):
     assert np.array_equal(bits(m.out), want)
 
 
-def test_a_captured_reduction_replays_like_eager_calls(ext):
+@pytest.mark.parametrize("n", [2048, 8 * 256 * 4 * 3 + 6, 81920 + 6, 256 * 8192])
+def test_a_captured_reduction_replays_like_eager_calls(ext, n):
     """The reduce records no memset and resets its own counters, so a HIP graph of it replays
-    right: several replays, with eager work and synchronisations between them, each checked."""
-    n, order = 8 * 256 * 4 * 3 + 6, [3, 1, 2]
+    right: several replays, with eager work and synchronisations between them, each checked. One
+    size per kernel: a grid of one (nothing counted), 12 workgroups (counted in the top word), 40
+    workgroups and C5 (counted in two levels, at 1 and 4 vectors a thread)."""
+    order = [3, 1, 2]
     inputs = {r: bf16_input(70 + r, n) for r in order}
     m = Members(inputs, order)
     m.publish(epoch=5)
