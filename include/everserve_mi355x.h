@@ -40,10 +40,13 @@ extern "C" {
 #define EVS_BOUND 12
 
 /* The local reduction's status word (evs_local_reduce, state[0]) once a call has finished:
- * (epoch << 16) | (reason << 8) | late_mask. */
+ * (epoch << 16) | (reason << 8) | late_mask, reason EVS_REDUCE_DONE or the bits below that
+ * apply (workgroups whose waits ended differently contribute each their own). */
 #define EVS_REDUCE_DONE 0      /* every member's flag carried the call's epoch */
 #define EVS_REDUCE_ABORTED 1   /* released by the ABORT control word */
 #define EVS_REDUCE_TIMED_OUT 2 /* the hard timeout passed with members still missing */
+#define EVS_REDUCE_BAD_ORDER 4 /* `order` named a row outside [0, EVS_MAX_ROWS): that position
+                                  added nothing, and the call did not wait for it */
 #define EVS_REDUCE_STATE_WORDS 288 /* state[0] the outcome; the rest the kernel's counters */
 
 /* The message of the last failed call on this thread ("" if none). */
@@ -174,7 +177,7 @@ int evs_order_pairs_static(const int64_t* slots, int64_t num_pairs, int key_bits
  * ctrl[EVS_BOUND] ns (0 = off), the kernel writes the mask of the rows it waits for into
  * ctrl[EVS_LATE], and the last block that named clears it when its wait ends. `state` (device
  * uint64 [EVS_REDUCE_STATE_WORDS], zeroed once before first use) receives in state[0], when the
- * call finishes, (epoch << 16) | (reason << 8) | late_mask with reason one of EVS_REDUCE_*; the
+ * call finishes, (epoch << 16) | (reason << 8) | late_mask with reason as above; the
  * other words are the kernel's own and return to zero at the end of every call, so a captured
  * HIP graph can replay it. Requires 0 <= n; out and every member buffer 2-byte aligned (16-byte
  * aligned takes the vector path). */

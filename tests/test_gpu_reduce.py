@@ -309,6 +309,23 @@ def test_a_captured_reduction_replays_like_eager_calls(ext, n):
         assert not m.state[1:].any()
 
 
+@pytest.mark.parametrize("n", [2048, 24576, 81920, 256 * 8192])
+def test_an_order_naming_a_row_out_of_range_adds_nothing_and_says_so(ext, n):
+    """Rows 9 and -1 in the order (outside [0, MAX_ROWS)) are not waited for and add nothing: the
+    sum equals the valid members' ordered sum, bit for bit, and the outcome carries reason
+    EVS_REDUCE_BAD_ORDER (4) through every counting mode: a grid of one, 12 workgroups (the top
+    word), 40 (two levels) and C5."""
+    inputs = {r: bf16_input(300 + r, n) for r in (0, 1)}
+    m = Members(inputs, [1, 0])
+    m.order.copy_(torch.tensor([4, 1, 9, 0, -1] + [0] * (MAXW - 4), dtype=torch.int32))
+    m.publish(epoch=6)
+    ext.local_reduce(m.bufs, m.flags, m.order, m.out, 6, 10**9, 0, m.state)
+    torch.cuda.synchronize()
+    assert m.status() == (6, 4, 0)
+    assert np.array_equal(bits(m.out), oracle.member_sum([bits(inputs[1]), bits(inputs[0])]))
+    assert not m.state[1:].any()
+
+
 @pytest.mark.parametrize("order", [[0], [0, 1], [1, 0, 2], [0, 3], [3, 0], [2, 0, 1, 3]])
 def test_special_values_round_as_the_oracle_does(ext, order):
     """Every bf16 pattern (signed zeros, subnormals, the largest values, infinities, NaNs), sums
