@@ -30,25 +30,25 @@
 //
 // The call's outcome is one word, state[0] = (epoch << 16) | (reason << 8) | late rows, written by
 // the last workgroup to count. Each workgroup counts once its wait is over, before its payload:
-// the outcome is settled then, and state[0] is read only after the kernel has completed.
-// Completion is counted in two levels of words. Workgroup b counts
-// in group word x = b mod G (G = min(8, workgroups), the words 256 bytes apart): it ORs its
-// outcome into the high bits and then adds 1 to the low bits, both relaxed atomics on that one
-// location, whose single modification order puts every outcome of the group before the last
-// add. The group's last workgroup carries the group's outcome the same way into the top word,
-// state[1], whose last adder then writes state[0]. No fence is needed, so no workgroup writes back
-// or invalidates the L2; and no word takes more than ceil(workgroups / G) + G of the atomics,
-// which on MI355X serialise per address at device scope (one word for every workgroup cost
-// 2.8 us of a 13 us call at 256 workgroups). A grid of at most EVS_REDUCE_FLAT_MAX workgroups
-// (decode sizes) counts straight into the top word instead, and a grid of one counts nothing: it
-// writes state[0] itself. The counting mode is a template parameter chosen at launch, so each
-// kernel holds only its own mode's code: on MI355X the code of modes a call does not run cost a
-// small grid 0.2-0.3 us, through the registers and schedule of its payload loop. The counting
-// words return to zero at the end of
-// every call, so the launch needs no memset and a captured graph can replay it. These atomics run
-// in one lane and their answers are read late; the file is built without the compiler's atomic
-// optimizer, whose wave-wide form of them would read each answer at once and so wait out the
-// round trip in front of the payload loads.
+// the outcome is settled then, and state[0] is read only after the kernel has completed. How a
+// call counts depends on its grid, and is a template parameter chosen at launch, so each kernel
+// holds only its own mode's code (on MI355X the code of modes a call does not run cost a small
+// grid 0.2-0.3 us, through the registers and schedule of its payload loop):
+//   - a grid of one counts nothing: it writes state[0] itself;
+//   - a grid of at most EVS_REDUCE_FLAT_MAX workgroups counts in the top word, state[1]: each
+//     workgroup ORs its outcome into the high bits and then adds 1 to the low bits, both relaxed
+//     atomics on that one location, whose single modification order puts every outcome before
+//     the last add; the last adder writes state[0];
+//   - a larger grid counts in two levels: workgroup b counts the same way in group word
+//     x = b mod 8 (the words 256 bytes apart), and each group's last workgroup carries the
+//     group's outcome into the top word. No word then takes more than ceil(workgroups / 8) + 8
+//     of the atomics, which on MI355X serialise per address at device scope (one word for every
+//     workgroup cost 2.8 us of a 13 us call at 256 workgroups).
+// No fence is needed, so no workgroup writes back or invalidates the L2. The counting words return
+// to zero at the end of every call, so the launch needs no memset and a captured graph can replay
+// it. These atomics run in one lane and their answers are read late; the file is built without
+// the compiler's atomic optimizer, whose wave-wide form of them would read each answer at once
+// and so wait out the round trip in front of the payload loads.
 
 #include "common.hpp"
 
@@ -99,15 +99,15 @@ constexpr int kCountTwoLevel = 2;
 constexpr int kGroupStride = 32;   // words between counting words (256 bytes)
 static_assert(kGroupStride * (1 + kGroups) <= EVS_REDUCE_STATE_WORDS, "state record too small");
 
+// The order of a thread's payload loads: 0 member by member, 1 vector by vector.
+#ifndef EVS_REDUCE_LOAD_ORDER
+#define EVS_REDUCE_LOAD_ORDER 1
+#endif
 // How the payload reads are ordered after the flags. 3 (default): every payload load is a buffer
 // load at agent scope (sc1), coherent on its own, so no cache is invalidated; issued after the
 // flag values returned, it sees what the producer wrote before releasing its flag. 1: one
 // acquire fence per workgroup (an L2 invalidate); 2: one per wave; 0: none, right only when every
 // payload was written before the launch.
-// The order of a thread's payload loads: 0 member by member, 1 vector by vector.
-#ifndef EVS_REDUCE_LOAD_ORDER
-#define EVS_REDUCE_LOAD_ORDER 1
-#endif
 #ifndef EVS_REDUCE_FENCE
 #define EVS_REDUCE_FENCE 3
 #endif
