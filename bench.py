@@ -621,6 +621,9 @@ def bench_c4(ext, steps, warmup):
     return {
         "config": "C4 restore: [32,8,262144,2,128] bf16 rows into a fresh 16384-block cache, "
                   "random-permutation block table (64 seqs x 4096 tokens)",
+        "paths": "scatter_* here: evs_scatter_rows with the rows in staged order; the Restorer "
+                 "(a restore from the store's tables) launches evs_scatter_ranges, measured in "
+                 "by_ranges_in_slot_order",
         "scatter_ms": round(ms, 3),
         "scatter_gbs": round(2 * payload / ms / 1e6, 1),
         "scatter_frac_of_8tbs": round(2 * payload / ms / 1e6 / PEAK_HBM_GBS, 4),
