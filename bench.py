@@ -109,11 +109,12 @@ def pinned_copy_gbs(nbytes, to_host, repeats=5):
 
 
 def pmc_traffic():
-    """HBM bytes per launch from the committed rocprofv3 counter profile, or None."""
+    """HBM bytes per launch from the committed rocprofv3 counter profile (its latest
+    measurement: the last traffic line), or None."""
     if not PMC_PROFILE.is_file():
         return None
-    m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.]+)", PMC_PROFILE.read_text(), re.M)
-    return float(m.group(1)) if m else None
+    found = re.findall(r"^traffic_bytes_per_launch:\s*([0-9.]+)", PMC_PROFILE.read_text(), re.M)
+    return float(found[-1]) if found else None
 
 
 # ------------------------------------------------------------------------------ C2 gather
