@@ -239,9 +239,13 @@ template <typename T, bool kNt, bool kSc1 = false>
 __device__ __forceinline__ void store_word(char* p, T v) {
   const global_ptr<T> g = (global_ptr<T>)(p);
   if constexpr (kNt && kSc1 && sizeof(T) == 16)
-    // no builtin sets the scope bits on a plain store; the word and the address are the asm's
-    // inputs, so the compiler waits for the loaded word before it, as for any store
-    asm volatile("global_store_dwordx4 %0, %1, off sc1 nt" : : "v"(g), "v"(v) : "memory");
+    // No builtin sets the scope bits on a plain store; the word and the address are the asm's
+    // inputs, so the compiler waits for the loaded word before it, as for any store. A store of
+    // more than 64 bits reads its data registers after it issues, so a VALU write to them needs
+    // one wait state after it; the compiler's hazard check does not see inside the asm, so the
+    // s_nop gives that wait state whatever is scheduled next.
+    asm volatile("global_store_dwordx4 %0, %1, off sc1 nt\n\ts_nop 0" : : "v"(g), "v"(v)
+                 : "memory");
   else if (kNt)
     __builtin_nontemporal_store(v, g);
   else

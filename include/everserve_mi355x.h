@@ -149,8 +149,8 @@ int evs_order_pairs(const int64_t* slots, int64_t num_pairs, int key_bits, int64
                     int64_t* rows_out, void* workspace, int64_t workspace_bytes, void* stream);
 
 /* evs_order_pairs without a workspace argument, for callers that cannot allocate device memory
- * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No
- * counterpart in the reference. Its scratch is a file-scope device array of
+ * (tight serving loops, harnesses that forbid hipMalloc). Not for HIP graph capture: see the
+ * memset below. No counterpart in the reference. Its scratch is a file-scope device array of
  * EVS_ORDER_STATIC_SCRATCH_BYTES that every GPU the library runs on holds until the process ends;
  * num_pairs is at most EVS_ORDER_STATIC_MAX_PAIRS (a larger call is refused with a message, and
  * nothing is enqueued). Calls on one GPU share that GPU's array: two calls that overlap on one GPU

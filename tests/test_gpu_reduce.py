@@ -47,6 +47,18 @@ class Ctrl:
         self.ext.host_free(self.host)
 
 
+def named(ctrl: Ctrl, rows_mask: int, within_s: float = 2.0) -> bool:
+    """Poll the host-mapped LATE word until it names every row of ``rows_mask``: the call has
+    found those members missing and is waiting for them (past BOUND), so their flags, written
+    after this, arrive during its wait rather than before its launch."""
+    deadline = time.perf_counter() + within_s
+    while time.perf_counter() < deadline:
+        if int(ctrl.words[LATE]) & rows_mask == rows_mask:
+            return True
+        time.sleep(0.0002)
+    return False
+
+
 class Members:
     """k member buffers in HBM, their flags, the order, and the call's state."""
 
@@ -208,6 +220,7 @@ def test_members_that_arrive_late_in_the_middle_of_the_order(ext, n):
     order positions among them. The second size takes three passes of the grid and ends in an
     element tail."""
     flags_host, flags_dev = ext.host_alloc_mapped(MAXW * 8)
+    ctrl = Ctrl(ext)
     try:
         words = (ctypes.c_int64 * MAXW).from_address(flags_host)
         order = [5, 3, 7, 0, 1, 6, 2, 4]
@@ -215,16 +228,22 @@ def test_members_that_arrive_late_in_the_middle_of_the_order(ext, n):
         m = Members(inputs, order)
         for r in order:
             words[r] = 0 if r in (0, 6) else 9
-        ext.local_reduce(m.bufs, flags_dev, m.order, m.out, 9, 3_000_000_000, 0, m.state)
-        time.sleep(0.01)
-        words[6] = 9
-        time.sleep(0.01)
-        words[0] = 9
+        ctrl.words[BOUND] = 100_000  # name the rows still awaited after 0.1 ms of waiting
+        ext.local_reduce(m.bufs, flags_dev, m.order, m.out, 9, 3_000_000_000, ctrl.dev, m.state)
+        try:
+            waited = named(ctrl, (1 << 0) | (1 << 6))
+            words[6] = 9
+            time.sleep(0.01)
+        finally:
+            words[6] = words[0] = 9
         torch.cuda.synchronize()
+        assert waited, "the call never named rows 0 and 6 as late: it did not wait for them"
         assert m.status() == (9, 0, 0)
+        assert int(ctrl.words[LATE]) == 0
         want = oracle.member_sum([bits(inputs[r]) for r in order])
         assert np.array_equal(bits(m.out), want)
     finally:
+        ctrl.close()
         ext.host_free(flags_host)
 
 
@@ -239,6 +258,7 @@ def test_grids_at_the_launch_thresholds(ext, n):
     switches. At each, every member in, then one of them arriving while the call waits, summed as
     the oracle does, with the counting words back at zero."""
     flags_host, flags_dev = ext.host_alloc_mapped(MAXW * 8)
+    ctrl = Ctrl(ext)
     try:
         words = (ctypes.c_int64 * MAXW).from_address(flags_host)
         order = [6, 1, 4, 0, 7, 2, 5, 3]
@@ -255,14 +275,20 @@ def test_grids_at_the_launch_thresholds(ext, n):
         for r in order:
             words[r] = 0 if r == 0 else 2
         torch.cuda.synchronize()
-        ext.local_reduce(m.bufs, flags_dev, m.order, m.out, 2, 3_000_000_000, 0, m.state)
-        time.sleep(0.01)
-        words[0] = 2
+        ctrl.words[BOUND] = 100_000
+        ext.local_reduce(m.bufs, flags_dev, m.order, m.out, 2, 3_000_000_000, ctrl.dev, m.state)
+        try:
+            waited = named(ctrl, 1 << 0)
+        finally:
+            words[0] = 2
         torch.cuda.synchronize()
+        assert waited, "the call never named row 0 as late: it did not wait for it"
         assert m.status() == (2, 0, 0)
+        assert int(ctrl.words[LATE]) == 0
         assert np.array_equal(bits(m.out), want)
         assert not m.state[1:].any()
     finally:
+        ctrl.close()
         ext.host_free(flags_host)
 
 

@@ -4,7 +4,7 @@ Its output must equal evs_order_pairs' (the entry point with a caller's workspac
 two calls in a row, the second smaller than the first, so that the scratch array still holds the
 first call's contents when the second runs. The slot lists hold padding ids and repeated slots,
 whose listed order the stable sort keeps. A call past the scratch's maximum is refused before
-anything is enqueued.
+anything is enqueued, and the first call on a device allocates no device memory.
 """
 
 import ctypes
@@ -45,6 +45,27 @@ def static(ext, slots, bits):
                                          out_r.data_ptr(), torch.cuda.current_stream().cuda_stream)
     assert rc == 0, ext._lib.evs_last_error()
     return out_s, out_r
+
+
+def test_the_first_call_allocates_no_device_memory(ext):
+    """The call's promise: no device memory is allocated, by it or lazily under it (the scratch
+    address looked up on the first call on a device, rocPRIM's first sort of a size). The
+    library's kernels are loaded first, by the workspace entry point; the free device memory and
+    torch's reserved memory are then the same after the first allocation-free call."""
+    slots = slot_list(300_000, 1 << 20, seed=5)
+    want = with_workspace(ext, slots, 20)
+    out_s, out_r = torch.empty_like(slots), torch.empty_like(slots)
+    torch.cuda.synchronize()
+    free_before, _ = torch.cuda.mem_get_info()
+    reserved_before = torch.cuda.memory_reserved()
+    rc = ext._lib.evs_order_pairs_static(slots.data_ptr(), slots.numel(), 20, out_s.data_ptr(),
+                                         out_r.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    free_after, _ = torch.cuda.mem_get_info()
+    assert rc == 0, ext._lib.evs_last_error()
+    assert torch.cuda.memory_reserved() == reserved_before
+    assert free_after == free_before, free_before - free_after
+    assert torch.equal(out_s, want[0]) and torch.equal(out_r, want[1])
 
 
 def test_the_scratch_holds_the_largest_call_it_takes(ext):
