@@ -27,6 +27,7 @@ chunk: no slot ids are built or copied. Rows land byte for byte where ``write_ro
 
 from __future__ import annotations
 
+import mmap
 import os
 import threading
 import time
@@ -74,7 +75,7 @@ class Table:
     ``StoreTables`` holds them, or a read-only mapping of the table file); ``written`` the
     ``(start, count)`` slot ranges the store names (proto/everserve/proto/mirror.proto:102-117).
     The mapping lives as long as the Table. On the hosts measured, unmapping 128 MiB of shared
-    memory costs 0.8-3.4 ms, as much as gathering it: drop the tables after the restore with
+    memory costs 0.7-3.4 ms, as much as gathering it: drop the tables after the restore with
     :func:`release_later`, or map them ahead of a failure and keep them mapped.
     """
 
@@ -92,8 +93,23 @@ class Table:
 
     @classmethod
     def open(cls, table: int, path: str, written: Sequence[tuple[int, int]]) -> "Table":
-        """The table file at ``path`` mapped read-only (its pages are read when gathered)."""
-        return cls(table, np.memmap(path, dtype=np.uint8, mode="r"), written)
+        """The table file at ``path`` mapped read-only (its pages are read when gathered).
+
+        The mapping is marked for sequential reading (``MADV_SEQUENTIAL``): a restore reads each
+        table once, front to back. Linux then leaves the pages' LRU state alone on this mapping's
+        faults and unmap; otherwise the first restore of freshly written tables moves their pages
+        to the active list, page by page under the LRU lock, which made the first unmap of
+        4 GiB of tables take 97-111 ms against 23-28 ms for later ones."""
+        with open(path, "rb") as f:
+            size = os.fstat(f.fileno()).st_size
+            if size == 0:
+                return cls(table, np.empty(0, dtype=np.uint8), written)
+            mapping = mmap.mmap(f.fileno(), size, flags=mmap.MAP_SHARED, prot=mmap.PROT_READ)
+        try:
+            mapping.madvise(mmap.MADV_SEQUENTIAL)
+        except (OSError, AttributeError):
+            pass  # an advice only: the copy is the same without it
+        return cls(table, np.frombuffer(mapping, dtype=np.uint8), written)
 
 
 def release_later(tables: list) -> threading.Thread:
@@ -114,14 +130,16 @@ def release_later(tables: list) -> threading.Thread:
 
 @dataclass
 class _Group:
-    """Tables of one layer with the same written ranges: scattered together, one launch a chunk."""
+    """Tables with the same written ranges, scattered together, one launch a chunk: the tables
+    of ``layers`` (one layer, or several that fit one chunk together), layer after layer, each
+    layer's in the order of ``heads``."""
 
-    layer: int
+    layers: list[int]
     starts: np.ndarray
     counts: np.ndarray
     tables: list[Table]
     heads: list[int]
-    """The head slot each table is written into, in the order of ``tables``."""
+    """The head slot each of a layer's tables is written into; the same for every layer."""
 
 
 class Restorer:
@@ -129,7 +147,8 @@ class Restorer:
 
     ``chunk_bytes`` is the rows one scatter launch writes over all of a group's tables, and
     ``piece_bytes`` the rows one host gather and one copy to the device carry; two pinned and two
-    device buffers of ``chunk_bytes`` are allocated once. On MI355X, inside a restore from
+    device buffers of ``chunk_bytes`` are allocated, and the pinned ones touched, once, here: a
+    spare builds its Restorer when it starts, before any failure. On MI355X, inside a restore from
     ``/dev/shm``, a scatter of 64 MiB ran at 4.9 TB/s, of 128 MiB at 5.4 and of 256 MiB at 5.7
     (a launch's ramp and tail weigh on the shorter ones), while the restore as a whole, bound by
     the PCIe copies, ran 0.5-1 % slower with 256 MiB copies than with 64 MiB ones, which fill and
@@ -177,10 +196,16 @@ class Restorer:
         # more, so a chunk of n rows has at most n ranges
         self._host_ranges = [torch.empty(2 * rows + 1, dtype=torch.long, pin_memory=True)
                              for _ in range(2)]
+        # The pinned buffers are touched here, every page, so that the first restore does not
+        # pay for it: the pinned allocator torch uses on ROCm backs its pages on first touch,
+        # which on MI355X hosts costs about 15 ms per 256 MiB (a later fill takes 3 ms).
+        for t in (*self._host, *self._host_ranges):
+            t.zero_()
         self._dev = [torch.empty(nb, dtype=torch.uint8, device=self.device) for _ in range(2)]
         self._dev_ranges = [torch.empty(2 * rows + 1, dtype=torch.long, device=self.device)
                             for _ in range(2)]
         self._heads: dict[tuple[int, ...], torch.Tensor] = {}
+        self._layer_ptrs: dict[tuple[int, ...], torch.Tensor] = {}
         self._copy_stream = torch.cuda.Stream(device=self.device)
         # per buffer: its last copy to the device (the pinned buffer is free after it) and its last
         # scatter (the device buffer is free after it)
@@ -194,6 +219,13 @@ class Restorer:
         if key not in self._heads:
             self._heads[key] = torch.tensor(key, dtype=torch.long, device=self.device)
         return self._heads[key]
+
+    def _layer_list(self, layers: Sequence[int]) -> torch.Tensor:
+        key = tuple(layers)
+        if key not in self._layer_ptrs:
+            self._layer_ptrs[key] = torch.tensor([self.layers[i].data_ptr() for i in key],
+                                                 dtype=torch.long, device=self.device)
+        return self._layer_ptrs[key]
 
     def plan(self, tables: Iterable[Table], head_map: Mapping[int, int]) -> list[_Group]:
         """Check every table against this rank's cache and group them; nothing is enqueued.
@@ -210,6 +242,7 @@ class Restorer:
         rb = self._row_bytes
         groups: dict[tuple, _Group] = {}
         taken: set[tuple[int, int]] = set()
+        ranges: dict[int, tuple[np.ndarray, np.ndarray]] = {}  # by the written list's identity
         for table in tables:
             if table.head not in head_map or not table.written:
                 continue
@@ -230,8 +263,11 @@ class Restorer:
             rows = table.rows
             if rows.nbytes % rb or (rows.ndim == 2 and rows.shape[1] * rows.itemsize != rb):
                 raise ValueError(f"{name}: not a whole number of this cache's {rb}-byte rows")
-            starts = np.array([s for s, _ in table.written], dtype=np.int64)
-            counts = np.array([c for _, c in table.written], dtype=np.int64)
+            got = ranges.get(id(table.written))
+            if got is None or got[2] is not table.written:
+                w = np.asarray(table.written, dtype=np.int64).reshape(-1, 2)
+                got = ranges[id(table.written)] = (w[:, 0].copy(), w[:, 1].copy(), table.written)
+            starts, counts = got[0], got[1]
             ends = starts + counts
             if (starts < 0).any() or (counts < 0).any() or ends.max() > rows.nbytes // rb:
                 raise ValueError(f"{name}: a written range lies outside the table")
@@ -245,10 +281,38 @@ class Restorer:
             key = (layer, starts.tobytes(), counts.tobytes(), rows.nbytes)
             g = groups.get(key)
             if g is None:
-                g = groups[key] = _Group(layer, starts, counts, [], [])
+                g = groups[key] = _Group([layer], starts, counts, [], [])
             g.tables.append(table)
             g.heads.append(head)
-        return list(groups.values())
+        return self._merge(list(groups.values()))
+
+    def _merge(self, groups: list[_Group]) -> list[_Group]:
+        """Join groups of different layers that have the same ranges, head slots and layout
+        strides into one group while their rows fit one chunk together: one launch then writes
+        them all. A catch-up after a few decode steps has a few MiB per layer, which one layer a
+        launch would spend on per-launch costs; a full restore's layers fill chunks by
+        themselves and stay apart."""
+        rb = self._row_bytes
+        by_key: dict[tuple, list[_Group]] = {}
+        for g in groups:
+            order = np.argsort(g.heads, kind="stable")
+            g.heads = [g.heads[i] for i in order]
+            g.tables = [g.tables[i] for i in order]
+            key = (g.starts.tobytes(), g.counts.tobytes(), g.tables[0].rows.nbytes,
+                   tuple(g.heads), tuple(self._strides[g.layers[0]]))
+            by_key.setdefault(key, []).append(g)
+        out: list[_Group] = []
+        for same in by_key.values():
+            rows = int(same[0].counts.sum())
+            one = rows * len(same[0].heads) * rb  # a layer's bytes
+            per = max(1, self._chunk_bytes // one) if one else 1
+            for i in range(0, len(same), per):
+                part = same[i:i + per]
+                out.append(_Group([layer for g in part for layer in g.layers], part[0].starts,
+                                  part[0].counts, [t for g in part for t in g.tables],
+                                  list(part[0].heads)))
+        out.sort(key=lambda g: g.layers[0])
+        return out
 
     def restore(self, tables: Iterable[Table], head_map: Mapping[int, int],
                 scales: Mapping[int, Sequence[float]] | None = None) -> int:
@@ -315,8 +379,8 @@ class Restorer:
         rb, k = self._row_bytes, len(g.tables)
         first_row = np.concatenate([[0], np.cumsum(g.counts)])
         rows = int(first_row[-1])
-        layer = g.layer
-        layer_ptr = self._ptrs[layer:layer + 1]
+        layer = g.layers[0]
+        layer_ptrs = self._layer_list(g.layers)
         heads = self._head_list(g.heads)
         srcs = [t.rows.ctypes.data for t in g.tables]
         table_rows = g.tables[0].rows.nbytes // rb
@@ -359,7 +423,7 @@ class Restorer:
                 self._copied[buf] = self._copy_stream.record_event()
             stream.wait_event(self._copied[buf])
             dr = self._dev_ranges[buf]
-            self._ext.scatter_ranges(layer_ptr, dr[:r], dr[r:2 * r + 1], n, heads, dev, n,
+            self._ext.scatter_ranges(layer_ptrs, dr[:r], dr[r:2 * r + 1], n, heads, dev, n,
                                      self.paged.head_dim, self.paged.block_size,
                                      self._strides[layer], self._elem)
             self._scattered[buf] = stream.record_event()

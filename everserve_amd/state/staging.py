@@ -329,6 +329,8 @@ class StepStager:
         self._bounce_bytes = int(bounce_bytes)
         self._bounce = [torch.empty(self._bounce_bytes, dtype=torch.uint8, pin_memory=True)
                         for _ in range(2)]
+        for b in self._bounce:  # backed on first touch: touched now, not in the first delivery
+            b.zero_()
         self._copy_threads = max(1, int(copy_threads))
         self._stage_seq = 0
         self._pool: list[Stage] = []

@@ -353,3 +353,45 @@ def test_random_restores_equal_the_oracle(ext, seed):
                                           max(1, live.size), d, bs, strides_of(src[0]), e)[0, 0]
             want[ours, live] = src_rows[:live.size]
         assert np.array_equal(back, want), (layer, moves)
+
+
+def test_layers_with_the_same_ranges_share_a_launch_unless_heads_or_layout_differ(ext):
+    """A catch-up's tables: every layer written at the same few slots. Layers with the same head
+    slots and layout are scattered together in one launch; a layer missing a head's table, or
+    laid out differently, keeps a launch of its own; a chunk too small for two layers keeps every
+    layer apart. Bytes as the oracle's, every other head slot untouched."""
+    nb, bs, h, d = 32, 4, 2, 8
+    kv = caches("kv_first", d, torch.bfloat16, n_layers=4, nb=nb, bs=bs, h=h, seed=91)
+    bf = caches("blocks_first", d, torch.bfloat16, n_layers=1, nb=nb, bs=bs, h=h, seed=92)
+    src = kv[:3] + bf + kv[3:]  # layer 3 is blocks_first
+    slots = [9, 10, 11, 40, 41, 77, 3]
+    t_kv, w_kv = commit(kv, slots, [0, 1], cap=8)
+    t_bf, w_bf = commit(bf, slots, [0, 1], cap=8)
+    tables = {}
+    for t, rows in t_kv.items():  # kv's layers 0, 1, 2, 3 are ours 0, 1, 2, 4
+        layer = t // 1000
+        tables[(layer if layer < 3 else 4) * 1000 + t % 1000] = (rows, w_kv[t])
+    for t, rows in t_bf.items():
+        tables[3000 + t % 1000] = (rows, w_bf[t])
+    del tables[1001]  # layer 1 has head 0's table only
+    moves = {0: 1, 1: 0}
+    for chunk_bytes, launches in ((1 << 20, 3), (len(slots) * 2 * 2 * d * 2, 5)):
+        dst = [torch.zeros_like(t).cuda() for t in src]
+        r = Restorer(ext, dst, chunk_bytes=chunk_bytes)
+        rows = r.restore([Table(t, tb, oracle.written_ranges(w)) for t, (tb, w) in tables.items()],
+                         moves)
+        assert rows == len(slots) * len(tables)
+        # layers 0, 2, 4 together (kv_first, both heads); layer 1 (one head); layer 3 (blocks_first)
+        assert r.timing["launches"] == launches
+        for layer, t in enumerate(dst):
+            cpu = t.cpu()
+            theirs = [x for x in (0, 1) if layer * 1000 + x in tables]
+            got = oracle.gather_rows([cpu], slots, [moves[x] for x in theirs], 8, d, bs,
+                                     strides_of(cpu), 2)
+            want = oracle.gather_rows([src[layer]], slots, theirs, 8, d, bs,
+                                      strides_of(src[layer]), 2)
+            assert np.array_equal(got, want), layer
+            if len(theirs) == 1:  # layer 1's head slot 0 (theirs 1) is not written
+                rest = oracle.gather_rows([cpu], list(range(nb * bs)), [0], nb * bs, d, bs,
+                                          strides_of(cpu), 2)
+                assert not rest.any()
