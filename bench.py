@@ -429,7 +429,8 @@ def bench_c3(ext, steps, warmup):
     del layers, staging
     torch.cuda.empty_cache()
     plain = pinned_copy_gbs(payload, to_host=True)
-    for k in ("deliver_gbs", "deliver_16_threads_gbs", "pageable_copy_gbs"):
+    for k in ("deliver_gbs", "deliver_16_threads_gbs", "deliver_from_own_thread_gbs",
+              "pageable_copy_gbs"):
         delivery[k.replace("_gbs", "_frac_of_plain_d2h")] = round(delivery[k] / plain, 4)
     g_ms, c_ms, b_ms = (sum(x) / len(x) for x in (g_per, c_per, b_per))
     return {
@@ -454,11 +455,17 @@ def bench_c3(ext, steps, warmup):
     }
 
 
-def c3_file_delivery(ext, staging, runs, run_bytes, dev, repeats=3):
+def c3_file_delivery(ext, staging, runs, run_bytes, dev, repeats=5):
     """The C3 rows from HBM into a staging file in shared memory, the store's side of the
     boundary: ``evs_deliver_rows`` (two 32 MiB pinned bounce buffers, host threads copying into
-    the file), and for comparison one pageable copy straight into the file's mapping."""
+    the file), and for comparison one pageable copy straight into the file's mapping.
+
+    Every repeat's time is kept, with the host's CPU set and threading environment, and the
+    delivery's two halves are timed apart: the host copy alone (the bounce buffer into the file
+    on the same threads, no copy engine at work) and the same delivery called from a thread of
+    its own, as the ``StepStager``'s copy thread calls it."""
     import tempfile
+    import threading
 
     import numpy as np
     import torch
@@ -474,34 +481,56 @@ def c3_file_delivery(ext, staging, runs, run_bytes, dev, repeats=3):
     side = torch.cuda.Stream(device=dev)
     view = np.frombuffer(mapping, dtype=np.uint8)
     addr = view.ctypes.data
-    out = {"file": str(path.parent), "bounce_bytes": bounce_bytes}
+    out = {"file": str(path.parent), "bounce_bytes": bounce_bytes,
+           "host": {"cpu_count": os.cpu_count(), "affinity_cpus": len(os.sched_getaffinity(0)),
+                    "threading_env": {k: v for k, v in sorted(os.environ.items())
+                                      if k.startswith(("OMP_", "GOMP_", "KMP_", "MKL_"))}}}
+
+    def deliver(threads):
+        ext.deliver_rows(addr, run_bytes, staging.data_ptr(), run_bytes, runs, run_bytes,
+                         [b.data_ptr() for b in bounce], bounce_bytes, side, threads)
+
+    def timed(fn, key):
+        times = []
+        for _ in range(repeats):
+            view[::1 << 20] = 0xEE
+            t0 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t0)
+        ms = sorted(times)[len(times) // 2] * 1e3
+        out[f"{key}_ms"] = round(ms, 3)
+        out[f"{key}_gbs"] = round(payload / ms / 1e6, 2)
+        out[f"{key}_repeats_ms"] = [round(t * 1e3, 2) for t in times]
+
     try:
         torch.cuda.synchronize()
         for threads, key in ((8, "deliver"), (16, "deliver_16_threads")):
-            times = []
-            for _ in range(repeats):
-                view[::1 << 20] = 0xEE
-                t0 = time.perf_counter()
-                ext.deliver_rows(addr, run_bytes, staging.data_ptr(), run_bytes, runs, run_bytes,
-                                 [b.data_ptr() for b in bounce], bounce_bytes, side, threads)
-                times.append(time.perf_counter() - t0)
-            ms = sorted(times)[len(times) // 2] * 1e3
-            out[f"{key}_ms"] = round(ms, 3)
-            out[f"{key}_gbs"] = round(payload / ms / 1e6, 2)
+            timed(lambda: deliver(threads), key)
+
+        def on_thread():
+            th = threading.Thread(target=deliver, args=(8,))
+            th.start()
+            th.join()
+
+        timed(on_thread, "deliver_from_own_thread")
+        # the host half alone: the bounce buffer copied into each 32 MiB of the file in turn, on
+        # the same 8 threads with the same stores, while no copy engine runs
+        per = bounce_bytes >> 20
+
+        def host_half():
+            for at in range(0, payload - bounce_bytes + 1, bounce_bytes):
+                ext.host_gather_ranges(bounce[0].data_ptr(), per, 1 << 20, [0], [per],
+                                       addr + at, per, 8)
+
+        timed(host_half, "host_copy_only")
         sample = np.r_[0:1 << 20, payload - (1 << 20):payload]
+        deliver(8)
         out["bytes_equal"] = bool(np.array_equal(view[sample],
                                                  staging.view(-1)[torch.from_numpy(sample).to(dev)]
                                                  .cpu().numpy()))
         # a pageable copy: the runtime stages it through its own buffers
         file_t = torch.frombuffer(mapping, dtype=torch.uint8)
-        times = []
-        for _ in range(repeats):
-            t0 = time.perf_counter()
-            file_t.copy_(staging.view(-1))
-            times.append(time.perf_counter() - t0)
-        ms = sorted(times)[len(times) // 2] * 1e3
-        out["pageable_copy_ms"] = round(ms, 3)
-        out["pageable_copy_gbs"] = round(payload / ms / 1e6, 2)
+        timed(lambda: file_t.copy_(staging.view(-1)), "pageable_copy")
         del file_t
     finally:
         del view
@@ -695,18 +724,19 @@ def bench_restore_host(ext, steps, warmup):
         written = [(0, n)]
         caches = [torch.zeros((2, NB, BS, H, D), dtype=torch.bfloat16, device=dev) for _ in range(L)]
         head_map = {h: (h + 3) % H for h in range(H)}
-        # Four restores, each opening (mapping) the tables afresh inside its timing, as the
-        # reference's procedure maps each file in its loop. The timing ends when the cache is
-        # written; the tables' mappings are then released on a thread of their own
-        # (release_later), timed apart and finished before the next restore starts. The first
-        # restore is cold and includes building the Restorer (its pinned and device buffers); the
-        # other three are the steady state, reported by their median.
+        # The Restorer (its pinned and device buffers) is built when the spare starts, before
+        # any failure, and timed apart. Then four restores, each opening (mapping) the tables
+        # afresh inside its timing, as the reference's procedure maps each file in its loop. The
+        # timing ends when the cache is written; the tables' mappings are then released on a
+        # thread of their own (release_later), timed apart and finished before the next restore
+        # starts. The first restore is cold; the other three are the steady state, reported by
+        # their median.
+        t0 = time.perf_counter()
+        restorer = Restorer(ext, caches)
+        build_s = time.perf_counter() - t0
         ours, release = [], []
-        restorer = None
         for _ in range(4):
             t0 = time.perf_counter()
-            if restorer is None:
-                restorer = Restorer(ext, caches)
             tables = [Table.open(t, p, written) for t, p in paths.items()]
             rows = restorer.restore(tables, head_map)
             ours.append(time.perf_counter() - t0)
@@ -765,10 +795,12 @@ def bench_restore_host(ext, steps, warmup):
         "payload_bytes": payload,
         "tables_dir": os.path.dirname(tmp),
         "timing": "4 restores each, every one opening the tables afresh inside its timing: the "
-                  "first cold (ours including building the Restorer), the steady state the "
-                  "median of the other 3. Ours ends when the cache is written; its tables' "
-                  "release is timed apart (release_later). The reference's procedure releases "
-                  "each table inside its loop, as written.",
+                  "first cold, the steady state the median of the other 3. Ours is built "
+                  "(restorer_build_ms) when the spare starts, before the first restore. Ours ends "
+                  "when the cache is written; its tables' release is timed apart "
+                  "(release_later). The reference's procedure releases each table inside its "
+                  "loop, as written.",
+        "restorer_build_ms": round(build_s * 1e3, 1),
         "ours_s": round(ours_s, 3),
         "ours_gbs": round(payload / ours_s / 1e9, 2),
         "reference_procedure_s": round(ref_s, 3),
@@ -779,6 +811,7 @@ def bench_restore_host(ext, steps, warmup):
         "ours_tables_mapped_ahead_gbs": round(payload / sorted(ahead)[1] / 1e9, 2),
         "first_restore": {
             "ours_gbs": round(payload / ours[0] / 1e9, 2),
+            "ours_with_build_gbs": round(payload / (ours[0] + build_s) / 1e9, 2),
             "ours_release_ms": round(release[0] * 1e3, 1),
             "reference_procedure_gbs": round(payload / ref[0] / 1e9, 2),
             "speedup": round(ref[0] / ours[0], 2),
@@ -789,6 +822,139 @@ def bench_restore_host(ext, steps, warmup):
         "host_threads": restorer._threads,
         "scatter_launches_per_restore": launches,
     }
+
+
+def catch_up_written(steps_since, seqs=64, num_blocks=16384, block_size=16, seed=6):
+    """The slots a decode run writes after a watermark, as the store's sorted (start, count)
+    ranges: ``seqs`` sequences, each holding ``num_blocks // seqs`` blocks of a seeded
+    random-permutation block table, each appending ``steps_since`` tokens from a position near
+    1024 (a different one per sequence, so the runs start inside blocks)."""
+    import numpy as np
+
+    rng = np.random.default_rng(seed)
+    table = rng.permutation(num_blocks).reshape(seqs, num_blocks // seqs)
+    p0 = 1024 + rng.integers(0, block_size, seqs)
+    pos = p0[:, None] + np.arange(steps_since)[None, :]
+    slots = np.sort((table[np.arange(seqs)[:, None], pos // block_size] * block_size
+                     + pos % block_size).reshape(-1))
+    cut = np.flatnonzero(np.diff(slots) != 1) + 1
+    first = slots[np.r_[0, cut]]
+    last = slots[np.r_[cut - 1, slots.size - 1]]
+    return slots, [(int(a), int(b - a + 1)) for a, b in zip(first, last)]
+
+
+def bench_restore_catch_up(ext, steps, warmup):
+    """The spare's catch-up restore at the swap (adapters/vllm/everserve_vllm/spare.py:163-192):
+    only the slots written after the first restore's watermark
+    (core/everserve/state/mirror.py:897-904), many short ranges per table. All 256 tables of a
+    Llama-3-8B rank ([262144, 2, 128] bf16 each, sparse /dev/shm files holding the written rows)
+    into a fresh 16384-block cache, ours against the reference's procedure on the same files."""
+    import shutil
+    import tempfile
+
+    import numpy as np
+    import torch
+
+    from everserve_amd.state.restore import Restorer, Table, release_later
+
+    L, NB, BS, H, D = 32, 16384, 16, 8, 128
+    n = NB * BS
+    row_bytes = 2 * D * 2
+    dev = torch.device("cuda", 0)
+    head_map = {h: (h + 3) % H for h in range(H)}
+    caches = [torch.zeros((2, NB, BS, H, D), dtype=torch.bfloat16, device=dev) for _ in range(L)]
+    restorer = Restorer(ext, caches)
+    out = {"config": f"catch-up restore of {L * H} store tables ([262144, 2, 128] bf16) into a "
+                     f"fresh 16384-block cache at other head slots: 64 sequences on a random "
+                     f"block table, the slots written in the last S decode steps",
+           "timing": "4 restores each, tables mapped afresh inside each timing; cold = the "
+                     "first, steady = the median of the other 3; ours ends when the cache is "
+                     "written (the mappings are released after, apart)"}
+    shm = "/dev/shm" if os.path.isdir("/dev/shm") else None
+    for since in (16, 256):
+        slots, written = catch_up_written(since, num_blocks=NB, block_size=BS)
+        rows_per_table = slots.size
+        payload = rows_per_table * row_bytes * L * H
+        if shm is not None and shutil.disk_usage(shm).free < payload + (256 << 20):
+            shm = None
+        tmp = tempfile.mkdtemp(prefix="evs-catchup-", dir=shm)
+        try:
+            blk = np.random.default_rng(since).integers(0, 1 << 16, size=(rows_per_table, 2 * D),
+                                                        dtype=np.uint16) & 0xBFFF
+            paths = {}
+            for layer in range(L):
+                for h in range(H):
+                    t = layer * 1000 + h
+                    paths[t] = os.path.join(tmp, f"table{t}.rows")
+                    with open(paths[t], "wb") as f:
+                        f.truncate(n * row_bytes)
+                    mm = np.memmap(paths[t], dtype=np.uint16, mode="r+", shape=(n, 2 * D))
+                    mm[slots] = blk ^ np.uint16(t & 0x3FFF)
+                    mm.flush()
+                    del mm
+            ours, release = [], []
+            for _ in range(4):
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                tables = [Table.open(t, p, written) for t, p in paths.items()]
+                got = restorer.restore(tables, head_map)
+                ours.append(time.perf_counter() - t0)
+                t0 = time.perf_counter()
+                release_later(tables).join()
+                release.append(time.perf_counter() - t0)
+            launches = restorer.timing.get("launches")
+            # check two tables' rows in their new head slots
+            ok = got == rows_per_table * L * H
+            s_dev = torch.from_numpy(slots).to(dev)
+            for t in (0 * 1000 + 5, 17 * 1000 + 2):
+                layer, h = divmod(t, 1000)
+                c = caches[layer][:, s_dev // BS, s_dev % BS, head_map[h]]  # [2, rows, D]
+                want = torch.from_numpy((blk ^ np.uint16(t & 0x3FFF)).view(np.int16)
+                                        .reshape(rows_per_table, 2, D).copy())
+                ok = ok and bool(torch.equal(c.transpose(0, 1).contiguous().view(torch.int16)
+                                             .cpu(), want))
+            # the reference's procedure (mirror.py:916-939) on the same files: per table,
+            # index_select of the written ranges into pinned memory, the copy, write_rows
+            idx = torch.cat([torch.arange(a, a + c, dtype=torch.long) for a, c in written])
+            ref = []
+            for _ in range(4):
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                for t, path in paths.items():
+                    layer, h = divmod(t, 1000)
+                    src = torch.from_file(path, shared=True, size=n * 2 * D,
+                                          dtype=torch.bfloat16).view(n, 2, D)
+                    pinned = torch.empty((idx.numel(), 2, D), dtype=torch.bfloat16,
+                                         pin_memory=True)
+                    torch.index_select(src, 0, idx, out=pinned)
+                    on_device = pinned.to(dev, non_blocking=True)
+                    i_dev = idx.to(dev)
+                    caches[layer][:, i_dev // BS, i_dev % BS, head_map[h]] = \
+                        on_device.transpose(0, 1)
+                torch.cuda.synchronize()
+                ref.append(time.perf_counter() - t0)
+        finally:
+            shutil.rmtree(tmp, ignore_errors=True)
+        o_s, r_s = sorted(ours[1:])[1], sorted(ref[1:])[1]
+        out[f"steps_{since}"] = {
+            "rows_per_table": int(rows_per_table),
+            "ranges_per_table": len(written),
+            "payload_bytes": int(payload),
+            "ours_ms": round(o_s * 1e3, 3),
+            "ours_gbs": round(payload / o_s / 1e9, 2),
+            "ours_first_ms": round(ours[0] * 1e3, 3),
+            "ours_release_ms": round(sorted(release[1:])[1] * 1e3, 2),
+            "reference_procedure_ms": round(r_s * 1e3, 3),
+            "reference_procedure_gbs": round(payload / r_s / 1e9, 2),
+            "reference_procedure_first_ms": round(ref[0] * 1e3, 3),
+            "speedup": round(r_s / o_s, 2),
+            "first_speedup": round(ref[0] / ours[0], 2),
+            "scatter_launches": launches,
+            "rows_check": bool(ok),
+        }
+    del caches, restorer
+    torch.cuda.empty_cache()
+    return out
 
 
 # ------------------------------------------------------------------------------ slot collective
@@ -1494,7 +1660,8 @@ def main(argv=None):
     legs = (("c1_gather", bench_c1), ("c2_layouts", bench_c2_layouts),
             ("c3_fp8_gather_d2h", bench_c3),
             ("c4_restore", bench_c4),
-            ("restore_host_path", bench_restore_host), ("store_commit", bench_store_commit),
+            ("restore_host_path", bench_restore_host),
+            ("restore_catch_up", bench_restore_catch_up), ("store_commit", bench_store_commit),
             ("c5_reduce", bench_c5),
             ("slot_all_reduce", bench_slot), ("decode_overhead", bench_decode_overhead))
     wanted = {x for x in a.legs.split(",") if x}
