@@ -49,12 +49,20 @@ namespace {
 #define EVS_SCATTER_VPT 2
 #endif
 // Per direction, bit 0: nontemporal loads, bit 1: nontemporal stores. Every byte here is touched
-// once, so no line is worth keeping in L2 or the Infinity Cache.
+// once, so no line is worth keeping in L2 or the Infinity Cache. For the scatter in staged order
+// the nontemporal row loads also keep the slot ids in L2: each of a slot range's 8 head tiles
+// reads them, far apart in time, and with plain row loads streaming through L2 every read missed
+// (HBM traffic 1.0078x the algorithmic bytes at C4; 1.00002x with the loads nontemporal, and
+// 5,646-5,657 against 5,627-5,653 GB/s, interleaved rounds on one box). The range scatter reads
+// no ids, and its nontemporal loads ran at 5,900 against 5,852 GB/s (C4, one box).
 #ifndef EVS_GATHER_NT
 #define EVS_GATHER_NT 3
 #endif
 #ifndef EVS_SCATTER_NT
-#define EVS_SCATTER_NT 2
+#define EVS_SCATTER_NT 3
+#endif
+#ifndef EVS_RANGES_NT
+#define EVS_RANGES_NT EVS_SCATTER_NT
 #endif
 // The gather's 16-byte stores also carry sc1, device scope: written through this XCD's L2, which
 // then holds no dirty lines of the staging buffer to write back later. Measured on MI355X (9
@@ -160,7 +168,10 @@ constexpr int vpt_of(int d, int i) {
   return i == kByPairs ? EVS_PAIRS_VPT : d == kGather ? EVS_GATHER_VPT : EVS_SCATTER_VPT;
 }
 constexpr int nt_of(int d, int i) {
-  return i == kByPairs ? EVS_PAIRS_NT : d == kGather ? EVS_GATHER_NT : EVS_SCATTER_NT;
+  return i == kByPairs    ? EVS_PAIRS_NT
+         : i == kByRanges  ? EVS_RANGES_NT
+         : d == kGather    ? EVS_GATHER_NT
+                           : EVS_SCATTER_NT;
 }
 constexpr int order_of(int d) { return d == kGather ? EVS_GATHER_ORDER : EVS_SCATTER_ORDER; }
 constexpr int word_order(int d, int i) { return i == kByPairs ? EVS_PAIRS_ORDER : order_of(d); }
