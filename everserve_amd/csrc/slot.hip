@@ -20,16 +20,16 @@
 // Waiting is bounded twice. Every 1024 polls a thread reads the member's ABORT control word
 // (core/csrc/slot.cu:174-175) and the wall clock; past `timeout_ns` it stops waiting by itself.
 // Thread 0 of each workgroup, past the BOUND word (ns), writes into LATE the rows it still waits
-// for: those of the batch it waits on, and for batches not reached yet, the rows whose first word
-// of this thread has not arrived (slot.cu:176-199). A counter after the sequence counters holds
-// the workgroups that named; the last to finish clears LATE. When a wait ends without a member,
-// that member's missing words are summed as zeros.
+// for: those of the group of members it waits on, and for groups not reached yet, the rows whose
+// first word of this thread has not arrived (slot.cu:176-199). A counter after the sequence
+// counters holds the workgroups that named; the last to finish clears LATE. When a wait ends
+// without a member, that member's missing words are summed as zeros.
 //
 // The launch is laid out for latency. Wave 0 reads the sequence counter, the order words and the
 // buffer table in one round of independent loads, one lane a word, while every thread loads its
 // input; the lanes then resolve, per order position, where the member's words are read and (push)
-// where this member's go, into LDS. A poll issues the loads of every member of a batch back to
-// back from those addresses and waits once, and a batch is every member (up to 8) at 1 or 2 words
+// where this member's go, into LDS. A poll issues the loads of every member of a group back to
+// back from those addresses and waits once, and a group is every member (up to 8) at 1 or 2 words
 // a thread, so a call of 8 members waits for one round trip a poll, not one per member.
 
 #include "common.hpp"
@@ -46,10 +46,10 @@ constexpr uint32_t kCheckEvery = 1024;
 
 // Members whose words a thread waits on together: every member (up to 8) at 1 or 2 words a
 // thread, 4 at more, where 8 members' words would hold 64-256 VGPRs. One round of loads then
-// covers a whole batch, so a call of k <= 8 members at 1 word a thread (the driver's setting)
-// waits for one round trip a poll, not one a batch.
+// covers a whole group, so a call of k <= 8 members at 1 word a thread (the driver's setting)
+// waits for one round trip a poll, not one a member.
 template <int W>
-constexpr int batch_of() {
+constexpr int group_of() {
   return W <= 2 ? kMaxRows : 4;
 }
 
@@ -68,12 +68,18 @@ struct SlotArgs {
   int64_t clock_khz;
 };
 
+// Every word these kernels read or write at system scope is global memory (device memory, or host
+// memory mapped for the device), so the accesses go through global_ rather than flat_
+// instructions: a flat store might alias LDS, and the compiler then waits for every such store to
+// complete before the next LDS read (which held each call's first poll behind its publish).
+typedef __attribute__((address_space(1))) uint64_t global_u64;
+
 __device__ __forceinline__ uint64_t load_sys(const uint64_t* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  return __hip_atomic_load((const global_u64*)(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 __device__ __forceinline__ void store_sys(uint64_t* p, uint64_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  __hip_atomic_store((global_u64*)(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 // A value the same in every lane, moved to scalar registers.
@@ -91,9 +97,136 @@ __device__ __forceinline__ uint32_t to_bf16(float f) {
   return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
 }
 
+// The words one thread reads for a group of up to G members of the order: word[q][j] is word j
+// of the group's q-th member (its buffer at src[q], its row row[q]); bit j of pending[q] stays set
+// until that word carries this call's number.
+template <int W, int G>
+struct Group {
+  int size;
+  const uint64_t* src[G];
+  int row[G];
+  uint64_t word[G][W];
+  uint32_t pending[G];
+};
+
+// One poll: every pending word of the group is loaded (all loads issued before any is tested),
+// and those that now carry `seq` stop pending. Returns whether any word still pends.
+template <int W, int G>
+__device__ __forceinline__ bool read_pending(Group<W, G>& g, int b0, uint32_t seq) {
+#pragma unroll
+  for (int q = 0; q < G; q++) {
+    if (g.pending[q] == 0) continue;
+#pragma unroll
+    for (int j = 0; j < W; j++)
+      if ((g.pending[q] >> j) & 1u) g.word[q][j] = load_sys(g.src[q] + b0 + j * kSlotThreads);
+  }
+  uint32_t still = 0;
+#pragma unroll
+  for (int q = 0; q < G; q++) {
+#pragma unroll
+    for (int j = 0; j < W; j++) {
+      const bool arrived = static_cast<uint32_t>(g.word[q][j] >> 32) == seq;
+      if (arrived) g.pending[q] &= ~(1u << j);
+    }
+    still |= g.pending[q];
+  }
+  return still != 0;
+}
+
+// The group's words added into the running sums, member after member in the group's order. A word
+// still pending (its member never came) adds +0.0, which changes no sum that started at +0.0.
+template <int W, int G>
+__device__ __forceinline__ void add_in_order(const Group<W, G>& g, float (&sum_lo)[W],
+                                             float (&sum_hi)[W]) {
+#pragma unroll
+  for (int q = 0; q < G; q++) {
+    if (q >= g.size) continue;
+#pragma unroll
+    for (int j = 0; j < W; j++) {
+      const bool use = ((g.pending[q] >> j) & 1u) == 0 && g.row[q] >= 0;
+      const uint32_t pair = use ? static_cast<uint32_t>(g.word[q][j]) : 0u;
+      sum_lo[j] += __uint_as_float(pair << 16);            // the low bf16, widened
+      sum_hi[j] += __uint_as_float(pair & 0xffff0000u);    // the high bf16, in place
+    }
+  }
+}
+
+// One thread's bounded wait over the whole call: when it started, the polls so far, whether it
+// gave up (ABORT or the timeout: later groups are then not waited for), and whether this
+// workgroup has named late rows (counted once in `namers`, the word after the sequence counters).
+struct Waiter {
+  int64_t start;
+  uint32_t polls;
+  bool gave_up;
+  bool named;
+  uint64_t* namers;
+
+  // Called after a poll that left words pending: false when the wait is over. Every kCheckEvery
+  // polls it reads ABORT and the clock; thread 0, past BOUND, also writes the rows it still
+  // waits for into LATE.
+  template <int W, int G>
+  __device__ __forceinline__ bool may_go_on(const SlotArgs& a, const Group<W, G>& g,
+                                            const uint64_t* const (&src_at)[kMaxRows],
+                                            const int (&row_at)[kMaxRows], int later, int b0,
+                                            uint32_t seq) {
+    if (++polls % kCheckEvery != 0) return true;
+    const int64_t waited = wall_clock64() - start;
+    const uint64_t* ctrl = reinterpret_cast<const uint64_t*>(a.ctrl);
+    if (load_sys(ctrl + EVS_ABORT) != 0 || waited > a.timeout_ticks) {
+      gave_up = true;
+      return false;
+    }
+    if (threadIdx.x == 0) {
+      const int64_t bound_ns = static_cast<int64_t>(load_sys(ctrl + EVS_BOUND));
+      if (bound_ns > 0 && waited * 1000000 / a.clock_khz > bound_ns)
+        name_late(a, late_rows(g, src_at, row_at, later, b0, seq));
+    }
+    return true;
+  }
+
+  // The rows this thread still waits for: in the current group, each member with a word pending;
+  // of the members in groups not reached yet (order positions from `later` on; an unlisted
+  // position has no address), each whose first word of this thread does not carry `seq`
+  // (core/csrc/slot.cu:176-199 names the same rows).
+  template <int W, int G>
+  __device__ __forceinline__ static int64_t late_rows(const Group<W, G>& g,
+                                                      const uint64_t* const (&src_at)[kMaxRows],
+                                                      const int (&row_at)[kMaxRows], int later,
+                                                      int b0, uint32_t seq) {
+    int64_t rows = 0;
+#pragma unroll
+    for (int q = 0; q < G; q++)
+      if (g.pending[q] != 0) rows |= int64_t{1} << g.row[q];
+#pragma unroll
+    for (int m = 0; m < kMaxRows; m++) {
+      if (m < later || src_at[m] == nullptr) continue;
+      if (static_cast<uint32_t>(load_sys(src_at[m] + b0) >> 32) != seq)
+        rows |= int64_t{1} << row_at[m];
+    }
+    return rows;
+  }
+
+  // Write LATE, counting this workgroup among the namers the first time. LATE is written at every
+  // check, since another workgroup's clear may have raced this one's earlier write.
+  __device__ __forceinline__ void name_late(const SlotArgs& a, int64_t rows) {
+    if (!named) {
+      __hip_atomic_fetch_add(namers, uint64_t{1}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      named = true;
+    }
+    store_sys(reinterpret_cast<uint64_t*>(a.ctrl + EVS_LATE), static_cast<uint64_t>(rows));
+  }
+
+  // The wait is over: the last namer to get here clears LATE.
+  __device__ __forceinline__ void done(const SlotArgs& a) {
+    if (named && __hip_atomic_fetch_add(namers, ~uint64_t{0}, __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT) == 1)
+      store_sys(reinterpret_cast<uint64_t*>(a.ctrl + EVS_LATE), 0);
+  }
+};
+
 template <int W, bool kPush>
 __global__ __launch_bounds__(kSlotThreads) void slot_all_reduce(SlotArgs a) {
-  constexpr int kBatch = batch_of<W>();
+  constexpr int kGroup = group_of<W>();
   // per order position q: the words this member reads (member q's, this call's parity half) and,
   // for push, where it writes its own into member q's buffer; null for a row out of range
   __shared__ const uint64_t* s_src[kMaxRows];
@@ -155,8 +288,17 @@ __global__ __launch_bounds__(kSlotThreads) void slot_all_reduce(SlotArgs a) {
   const uint32_t seq = s_seq;
   const int nmem = s_n;
   const uint64_t tag = static_cast<uint64_t>(seq) << 32;
+  // Every order position's read address and row, out of LDS into scalar registers once, before
+  // the first store: an LDS read behind outstanding stores may have to wait for them.
+  const uint64_t* src_at[kMaxRows];
+  int row_at[kMaxRows];
+#pragma unroll
+  for (int q = 0; q < kMaxRows; q++) {
+    src_at[q] = q < nmem ? uniform_ptr(s_src[q]) : nullptr;
+    row_at[q] = q < nmem ? __builtin_amdgcn_readfirstlane(s_row[q]) : -1;
+  }
 
-  // publish this member's words
+  // publish this member's words (push: into every member's buffer, one member at a time)
   if (kPush) {
     for (int q = 0; q < nmem; q++) {
       uint64_t* dst = uniform_ptr(s_dst[q]);
@@ -176,106 +318,42 @@ __global__ __launch_bounds__(kSlotThreads) void slot_all_reduce(SlotArgs a) {
     }
   }
 
-  float lo[W], hi[W];
-  uint32_t valid = 0;
+  // Members are taken in the listed order, a group of up to kGroup at a time: the group's words
+  // are read until they all carry this call's number (or the wait is given up), then added into
+  // the running sums. Bit j of `owned` is set when this thread has a word j.
+  uint32_t owned = 0;
+  float sum_lo[W], sum_hi[W];  // running fp32 sums of each word's low and high bf16
 #pragma unroll
   for (int j = 0; j < W; j++) {
-    lo[j] = 0.f;
-    hi[j] = 0.f;
-    if (b0 + j * kSlotThreads < a.n2) valid |= 1u << j;
+    sum_lo[j] = sum_hi[j] = 0.f;
+    if (b0 + j * kSlotThreads < a.n2) owned |= 1u << j;
   }
-  const bool watch = threadIdx.x == 0;
-  const int64_t t0 = wall_clock64();
-  bool counted = false;
-  bool released = false;  // by ABORT or the timeout: later batches are not waited for
-  uint32_t polls = 0;
-  uint64_t* late_count = reinterpret_cast<uint64_t*>(a.seqs + a.late_index);
-
-  for (int b = 0; b < nmem; b += kBatch) {
-    const uint64_t* src[kBatch];
-    int ms[kBatch];
-    const int nm = nmem - b < kBatch ? nmem - b : kBatch;
-    uint64_t w[kBatch][W];
-    uint32_t todo[kBatch];
+  Waiter waiter{wall_clock64(), 0u, false, false,
+                reinterpret_cast<uint64_t*>(a.seqs + a.late_index)};
 #pragma unroll
-    for (int q = 0; q < kBatch; q++) {
-      src[q] = q < nm ? uniform_ptr(s_src[b + q]) : nullptr;
-      ms[q] = q < nm ? __builtin_amdgcn_readfirstlane(s_row[b + q]) : -1;
-      todo[q] = (src[q] != nullptr && !released) ? valid : 0u;
+  for (int first = 0; first < kMaxRows; first += kGroup) {  // unrolled: every index is static
+    if (first >= nmem) break;
+    Group<W, kGroup> g;
+    g.size = nmem - first < kGroup ? nmem - first : kGroup;
 #pragma unroll
-      for (int j = 0; j < W; j++) w[q][j] = 0ull;
+    for (int q = 0; q < kGroup; q++) {
+      g.src[q] = src_at[first + q];
+      g.row[q] = row_at[first + q];
+      g.pending[q] = g.src[q] != nullptr && !waiter.gave_up ? owned : 0u;
+#pragma unroll
+      for (int j = 0; j < W; j++) g.word[q][j] = 0ull;  // a word never read adds +0.0
     }
-    while (true) {
-#pragma unroll
-      for (int q = 0; q < kBatch; q++) {
-        if (!todo[q]) continue;
-#pragma unroll
-        for (int j = 0; j < W; j++)
-          if (todo[q] >> j & 1) w[q][j] = load_sys(src[q] + b0 + j * kSlotThreads);
-      }
-      uint32_t any = 0;
-#pragma unroll
-      for (int q = 0; q < kBatch; q++) {
-#pragma unroll
-        for (int j = 0; j < W; j++)
-          if ((todo[q] >> j & 1) && static_cast<uint32_t>(w[q][j] >> 32) == seq)
-            todo[q] &= ~(1u << j);
-        any |= todo[q];
-      }
-      if (!any) break;
-      if ((++polls % kCheckEvery) == 0) {
-        const int64_t waited = wall_clock64() - t0;
-        const uint64_t* c = reinterpret_cast<const uint64_t*>(a.ctrl);
-        if (load_sys(c + EVS_ABORT) != 0 || waited > a.timeout_ticks) {
-          released = true;
-          break;
-        }
-        if (watch) {
-          const int64_t bound = static_cast<int64_t>(load_sys(c + EVS_BOUND));
-          if (bound > 0 && waited * 1000000 / a.clock_khz > bound) {
-            // the rows of this batch it still waits on, and of the batches after it, the rows
-            // whose first word of this thread has not arrived
-            int64_t late = 0;
-#pragma unroll
-            for (int q = 0; q < kBatch; q++)
-              if (todo[q]) late |= int64_t{1} << ms[q];
-            for (int q = b + nm; q < nmem; q++) {
-              const uint64_t* p = s_src[q];
-              if (p == nullptr) continue;
-              if (static_cast<uint32_t>(load_sys(p + b0) >> 32) != seq)
-                late |= int64_t{1} << s_row[q];
-            }
-            if (!counted) {
-              __hip_atomic_fetch_add(late_count, uint64_t{1}, __ATOMIC_RELAXED,
-                                     __HIP_MEMORY_SCOPE_AGENT);
-              counted = true;
-            }
-            store_sys(reinterpret_cast<uint64_t*>(a.ctrl + EVS_LATE), static_cast<uint64_t>(late));
-          }
-        }
-      }
+    while (read_pending(g, b0, seq)) {
+      if (!waiter.may_go_on(a, g, src_at, row_at, first + kGroup, b0, seq)) break;
       __builtin_amdgcn_s_sleep(1);
     }
-    // sum the batch in order; a word that never arrived, or a row out of range, counts as zero
-#pragma unroll
-    for (int q = 0; q < kBatch; q++) {
-      if (q >= nm) continue;
-#pragma unroll
-      for (int j = 0; j < W; j++) {
-        const uint32_t v = (todo[q] >> j & 1) || ms[q] < 0 ? 0u : static_cast<uint32_t>(w[q][j]);
-        lo[j] += __uint_as_float((v & 0xffffu) << 16);
-        hi[j] += __uint_as_float(v & 0xffff0000u);
-      }
-    }
+    add_in_order(g, sum_lo, sum_hi);
   }
-  // the wait is over; the last workgroup that named clears the word
-  if (counted && __hip_atomic_fetch_add(late_count, ~uint64_t{0}, __ATOMIC_RELAXED,
-                                        __HIP_MEMORY_SCOPE_AGENT) == 1)
-    store_sys(reinterpret_cast<uint64_t*>(a.ctrl + EVS_LATE), 0);
+  waiter.done(a);
 #pragma unroll
   for (int j = 0; j < W; j++) {
     const int i = b0 + j * kSlotThreads;
-    if (i < a.n2) a.out[i] = to_bf16(lo[j]) | (to_bf16(hi[j]) << 16);
+    if (i < a.n2) a.out[i] = to_bf16(sum_lo[j]) | (to_bf16(sum_hi[j]) << 16);
   }
 }
 
