@@ -478,6 +478,8 @@ def c3_file_delivery(ext, staging, runs, run_bytes, dev, repeats=5):
     mapping = _map_stage_file(path, payload)
     bounce_bytes = 32 << 20
     bounce = [torch.empty(bounce_bytes, dtype=torch.uint8, pin_memory=True) for _ in range(2)]
+    for b in bounce:  # touched once, as the StepStager does when it is built
+        b.zero_()
     side = torch.cuda.Stream(device=dev)
     view = np.frombuffer(mapping, dtype=np.uint8)
     addr = view.ctypes.data

@@ -423,9 +423,11 @@ __device__ __forceinline__ void finish_call(const ReduceArgs& a,
     for (int q = 0; q < count; q++) {
       uint32_t b = 0;
       if (src[q] != nullptr)
-        b = EVS_REDUCE_FENCE == 3 ? __hip_atomic_load(reinterpret_cast<const uint16_t*>(src[q] + e),
-                                                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                                  : src[q][e];
+        // a global load, not a flat one: member buffers are never LDS
+        b = EVS_REDUCE_FENCE == 3
+                ? __hip_atomic_load((const __attribute__((address_space(1))) uint16_t*)(src[q] + e),
+                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                : src[q][e];
       acc += bf16_to_f32(b);
     }
     a.out[e] = static_cast<uint16_t>(f32_to_bf16(acc));
