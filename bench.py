@@ -736,12 +736,15 @@ def bench_restore_host(ext, steps, warmup):
         t0 = time.perf_counter()
         restorer = Restorer(ext, caches)
         build_s = time.perf_counter() - t0
-        ours, release = [], []
+        ours, release, opened, parts = [], [], [], []
         for _ in range(4):
             t0 = time.perf_counter()
             tables = [Table.open(t, p, written) for t, p in paths.items()]
+            opened.append(time.perf_counter() - t0)
             rows = restorer.restore(tables, head_map)
             ours.append(time.perf_counter() - t0)
+            parts.append({k: round(v * 1e3, 2) for k, v in restorer.timing.items()
+                          if k.endswith("_s")})
             t0 = time.perf_counter()
             release_later(tables).join()
             release.append(time.perf_counter() - t0)
@@ -803,6 +806,8 @@ def bench_restore_host(ext, steps, warmup):
                   "(release_later). The reference's procedure releases each table inside its "
                   "loop, as written.",
         "restorer_build_ms": round(build_s * 1e3, 1),
+        "ours_open_ms": [round(x * 1e3, 2) for x in opened],
+        "ours_parts_ms": parts,
         "ours_s": round(ours_s, 3),
         "ours_gbs": round(payload / ours_s / 1e9, 2),
         "reference_procedure_s": round(ref_s, 3),
@@ -894,13 +899,16 @@ def bench_restore_catch_up(ext, steps, warmup):
                     mm[slots] = blk ^ np.uint16(t & 0x3FFF)
                     mm.flush()
                     del mm
-            ours, release = [], []
+            ours, release, opened, parts = [], [], [], []
             for _ in range(4):
                 torch.cuda.synchronize()
                 t0 = time.perf_counter()
                 tables = [Table.open(t, p, written) for t, p in paths.items()]
+                opened.append(time.perf_counter() - t0)
                 got = restorer.restore(tables, head_map)
                 ours.append(time.perf_counter() - t0)
+                parts.append({k: round(v * 1e3, 2) for k, v in restorer.timing.items()
+                              if k.endswith("_s")})
                 t0 = time.perf_counter()
                 release_later(tables).join()
                 release.append(time.perf_counter() - t0)
@@ -945,6 +953,8 @@ def bench_restore_catch_up(ext, steps, warmup):
             "ours_ms": round(o_s * 1e3, 3),
             "ours_gbs": round(payload / o_s / 1e9, 2),
             "ours_first_ms": round(ours[0] * 1e3, 3),
+            "ours_open_ms": [round(x * 1e3, 2) for x in opened],
+        "ours_parts_ms": parts,
             "ours_release_ms": round(sorted(release[1:])[1] * 1e3, 2),
             "reference_procedure_ms": round(r_s * 1e3, 3),
             "reference_procedure_gbs": round(payload / r_s / 1e9, 2),
@@ -952,6 +962,7 @@ def bench_restore_catch_up(ext, steps, warmup):
             "speedup": round(r_s / o_s, 2),
             "first_speedup": round(ref[0] / ours[0], 2),
             "scatter_launches": launches,
+            "ours_parts_ms": parts,
             "rows_check": bool(ok),
         }
     del caches, restorer

@@ -185,6 +185,7 @@ class Restorer:
                                 chunk_bytes // self._row_bytes * self._row_bytes)
         self._piece_bytes = min(self._chunk_bytes, max(self._row_bytes, int(piece_bytes)))
         self._launches = 0
+        self._gather_s = self._wait_s = 0.0
         self._threads = threads or min(16, len(os.sched_getaffinity(0)))
         self.scales = scales
         if scales is not None and (scales.device != self.device or scales.dtype != torch.float32
@@ -343,6 +344,7 @@ class Restorer:
         total = 0
         buf = 0
         self._launches = 0
+        self._gather_s = self._wait_s = 0.0
         for g in groups:
             rows, buf = self._restore_group(g, stream, buf)
             total += rows * len(g.tables)
@@ -350,10 +352,13 @@ class Restorer:
             with torch.inference_mode():
                 for layer, v in side.items():
                     self.scales[layer].copy_(torch.from_numpy(v), non_blocking=False)
+        t1 = time.perf_counter()
         torch.cuda.synchronize(self.device)
+        t2 = time.perf_counter()
         rb = self._row_bytes
-        self.timing = {"copy_s": time.perf_counter() - t0, "rows": total, "bytes": total * rb,
-                       "launches": self._launches}
+        self.timing = {"copy_s": t2 - t0, "rows": total, "bytes": total * rb,
+                       "launches": self._launches, "host_gather_s": self._gather_s,
+                       "buffer_wait_s": self._wait_s, "final_sync_s": t2 - t1}
         return total
 
     @staticmethod
@@ -393,7 +398,9 @@ class Restorer:
             c1 = min(rows, c0 + per_chunk)
             n = c1 - c0
             if self._copied[buf] is not None:
+                w0 = time.perf_counter()
                 self._copied[buf].synchronize()  # the copies out of this pinned buffer are done
+                self._wait_s += time.perf_counter() - w0
             host, dev = self._host[buf].data_ptr(), self._dev[buf].data_ptr()
             # the chunk is [k, n, 2, d]: staged rows of k head slots at capacity n; a piece is
             # rows [p0, p1) of every table, k runs n rows apart
@@ -401,8 +408,10 @@ class Restorer:
                 p1 = min(c1, p0 + per_piece)
                 st, ct = self._ranges(g, first_row, p0, p1)
                 off = (p0 - c0) * rb
+                g0 = time.perf_counter()
                 got = self._ext.host_gather_tables(srcs, table_rows, rb, st, ct, host + off, n,
                                                    self._threads)
+                self._gather_s += time.perf_counter() - g0
                 if got != p1 - p0:
                     raise RuntimeError(f"layer {layer}: gathered {got} rows of [{p0}, {p1})")
                 with torch.cuda.stream(self._copy_stream):

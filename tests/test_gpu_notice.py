@@ -1,8 +1,8 @@
 """Notice rounds on the GPU: a doomed rank's cache staged block round by block round, then restored.
 
-The reference's scenario (core/tests/test_staging.py:1-116) is a cache written token by token while
-rounds copy the blocks that changed. Here the cache is on the GPU, every layer and head slot, and
-each round goes through the product path:
+A decoding batch (test_oracle_staging.Batch's block bookkeeping) writes its KV into a GPU cache,
+every layer and head slot, while rounds copy the blocks that changed (the plan of
+core/everserve/reference/staging.py:51-94). Each round goes through the product path:
 1. ``StepStager.stage_round`` plans the round and gathers the blocks with the slot tags.
 2. The rows are delivered into the round's staging file in the rank directory.
 3. The oracle's store commit maps that file by its name and copies the rows into tables
@@ -10,11 +10,9 @@ each round goes through the product path:
 
 After the last round the product ``Restorer`` writes the tables' written ranges into a fresh cache
 (core/everserve/state/mirror.py:916-937). The fresh cache must equal the doomed one on every block
-in use, bit for bit. Also checked: each round's block ids are those the reference's planner picks,
+in use, bit for bit. Also checked: each round's block ids are those the oracle's planner picks,
 and the tags the kernel wrote are ``block * block_size + [0, block_size)``.
 """
-
-import random
 
 import numpy as np
 import pytest
@@ -24,57 +22,41 @@ import oracle
 from everserve_amd.state import notice, staging
 from everserve_amd.state.restore import Restorer, Table
 from tests.cases import bits
+from tests.test_oracle_staging import BLOCK as BS
+from tests.test_oracle_staging import Batch
 
 pytestmark = pytest.mark.gpu
 
-L, NB, BS, H, D = 3, 64, 16, 3, 8
+L, NB, H, D = 3, 64, 3, 8
 HEADS = [0, 2]
 
 
-class GpuCache:
-    """Block tables on the host, the KV on the GPU (kv_first bf16), written token by token."""
+class GpuBatch(Batch):
+    """The batch's KV in a kv_first bf16 cache on the GPU: a token's values for every layer and
+    head slot are drawn from a generator seeded by its (request, generation, position) value, so
+    a recomputed request writes new values."""
 
-    def __init__(self, n_req, prompt, seed):
-        self.rng = random.Random(seed)
-        self.free = list(range(NB))
-        self.rng.shuffle(self.free)
-        self.tables = {str(i): [] for i in range(n_req)}
-        self.n = {str(i): 0 for i in range(n_req)}
+    def __init__(self, prompts, seed):
         self.layers = [torch.zeros((2, NB, BS, H, D), dtype=torch.bfloat16, device="cuda")
                        for _ in range(L)]
-        for rid in self.tables:
-            self.write(rid, prompt)
+        super().__init__(prompts, seed, pool_blocks=NB)
 
-    def write(self, rid, k):
-        for _ in range(k):
-            pos = self.n[rid]
-            if pos // BS >= len(self.tables[rid]):
-                self.tables[rid].append(self.free.pop())
-            b = self.tables[rid][pos // BS]
-            # a token's KV depends on (request, position) only, as in the reference's mock: a
-            # recomputed request writes the same values again
-            g = torch.Generator().manual_seed(int(rid) * 100_003 + pos)
-            vals = torch.randn((L, 2, H, D), generator=g).to(torch.bfloat16).cuda()
-            for layer, t in enumerate(self.layers):
-                t[:, b, pos % BS] = vals[layer]
-            self.n[rid] += 1
+    def on_token(self, b, offset, r, t):
+        super().on_token(b, offset, r, t)
+        g = torch.Generator().manual_seed(self.value(r, t) % (1 << 62))
+        vals = torch.randn((L, 2, H, D), generator=g).to(torch.bfloat16).cuda()
+        for layer, cache in enumerate(self.layers):
+            cache[:, b, offset] = vals[layer]
 
-    def preempt(self, rid):
-        n = self.n[rid]
-        for b in self.tables[rid]:
-            for t in self.layers:
-                t[:, b].zero_()
-            self.free.append(b)
-        self.tables[rid], self.n[rid] = [], 0
-        self.rng.shuffle(self.free)
-        self.write(rid, n)
-
-    def in_use(self):
-        return sorted(b for t in self.tables.values() for b in t)
+    def release(self, r):
+        for b in self.blocks[r]:
+            for cache in self.layers:
+                cache[:, b].zero_()
+        super().release(r)
 
 
 def test_rounds_then_restore_rebuild_every_block_in_use(ext):
-    c = GpuCache(4, 37, seed=7)
+    c = GpuBatch({"a": 29, "b": 50, "c": 8, "d": 33}, seed=7)
     names = [f"model.layers.{i}.self_attn.attn" for i in range(L)]
     tables, written, tags = {}, {}, []
 
@@ -90,18 +72,18 @@ def test_rounds_then_restore_rebuild_every_block_in_use(ext):
     shadow = {}
     with staging.StepStager(ext, dict(zip(names, c.layers)), HEADS, sink) as st:
         for rnd in range(1, 9):
-            want_ids = oracle.blocks_to_stage(c.tables, dict(c.n), shadow, BS)
-            ids = st.stage_round(window, c.tables, dict(c.n), epoch=1, step=rnd)
+            want_ids = oracle.blocks_to_stage(c.blocks, dict(c.length), shadow, BS)
+            ids = st.stage_round(window, c.blocks, dict(c.length), epoch=1, step=rnd)
             assert ids == want_ids
             st.flush()
             if ids:
                 assert tags[-1] == oracle.expand_blocks(ids, BS).tolist()
             # the rank keeps serving: tokens, a preemption, a multi-token step
-            for rid in c.n:
-                c.write(rid, 1 if rnd % 3 else 17)
+            for r in c.length:
+                c.append(r, 1 if rnd % 3 else 17)
             if rnd == 4:
-                c.preempt("2")
-        ids = st.stage_round(window, c.tables, dict(c.n), epoch=1, step=9)
+                c.recompute("c")
+        ids = st.stage_round(window, c.blocks, dict(c.length), epoch=1, step=9)
         st.flush()
     assert window.rounds == 9 and window.blocks_copied > 0
     # the replacement: a fresh cache written from the tables' written ranges, head for head

@@ -1,10 +1,10 @@
 """The product's notice-round planner against the oracle's, on the CPU.
 
 ``everserve_amd.state.notice.blocks_to_stage`` is the product's. The oracle's restatement of the
-reference (core/everserve/reference/staging.py:51-94) is pinned by the reference's own scenarios
-in test_oracle_staging.py. The two are run here side by side over seeded random histories: decode
-and multi-token steps, prefills of new requests, preemptions into new blocks and finished
-requests. The same block ids and the same staged state are wanted after every round.
+reference (core/everserve/reference/staging.py:51-94) is pinned in test_oracle_staging.py. The two
+are run here side by side over seeded random histories of that file's simulated batch: decode and
+multi-token steps, prefills of new requests, preemptions into new blocks and finished requests.
+The same block ids and the same staged state are wanted after every round.
 """
 
 import random
@@ -13,7 +13,7 @@ import pytest
 
 import oracle
 from everserve_amd.state import notice
-from tests.test_oracle_staging import Cache
+from tests.test_oracle_staging import BLOCK, Batch
 
 
 def as_oracle(staged):
@@ -23,28 +23,26 @@ def as_oracle(staged):
 @pytest.mark.parametrize("seed", range(12))
 def test_the_plan_is_the_oracles_round_after_round(seed):
     rng = random.Random(seed)
-    bs = 16
-    c = Cache(rng.randrange(1, 6), rng.randrange(1, 40), seed=seed)
+    batch = Batch({f"q{i}": rng.randrange(1, 40) for i in range(rng.randrange(1, 6))}, seed=seed,
+                  pool_blocks=128)
     ours, theirs = {}, {}
-    next_id = len(c.tables)
+    admitted = len(batch.blocks)
     for _ in range(30):
-        got = notice.blocks_to_stage(c.tables, dict(c.n), ours, bs)
-        want = oracle.blocks_to_stage(c.tables, dict(c.n), theirs, bs)
+        got = notice.blocks_to_stage(batch.blocks, dict(batch.length), ours, BLOCK)
+        want = oracle.blocks_to_stage(batch.blocks, dict(batch.length), theirs, BLOCK)
         assert got == want
         assert as_oracle(ours) == theirs
         event = rng.random()
-        if event < 0.1 and c.n:
-            c.preempt(rng.choice(sorted(c.n)))
-        elif event < 0.2 and len(c.n) > 1:
-            c.finish(rng.choice(sorted(c.n)))
-        elif event < 0.3 and len(c.free) > 8:
-            rid = str(next_id)
-            next_id += 1
-            c.tables[rid], c.n[rid] = [], 0
-            c.write(rid, rng.randrange(1, 20))
-        for rid in list(c.n):
-            if len(c.free) > 4:
-                c.write(rid, rng.choice((1, 1, 1, 2, 17)))
+        if event < 0.1 and batch.length:
+            batch.recompute(rng.choice(sorted(batch.length)))
+        elif event < 0.2 and len(batch.length) > 1:
+            batch.finish(rng.choice(sorted(batch.length)))
+        elif event < 0.3 and len(batch.pool) > 8:
+            batch.admit(f"q{admitted}", rng.randrange(1, 20))
+            admitted += 1
+        for r in list(batch.length):
+            if len(batch.pool) > 4:
+                batch.append(r, rng.choice((1, 1, 1, 2, 17)))
 
 
 def test_the_window_counts_down_to_the_deadline():

@@ -22,21 +22,31 @@ POOL = 96
 
 class Batch:
     """A paged cache under decoding requests: each request owns a list of block ids taken from a
-    seeded free pool, and its token t lives at offset t % BLOCK of its (t // BLOCK)-th block."""
+    seeded free pool, and its token t lives at offset t % BLOCK of its (t // BLOCK)-th block.
+    Other tests build on it (the product planner's pins, the GPU notice rounds)."""
 
-    def __init__(self, prompts: dict[str, int], seed: int):
+    def __init__(self, prompts: dict[str, int], seed: int, pool_blocks: int = POOL):
         self.rng = np.random.default_rng(seed)
-        self.pool = [int(b) for b in self.rng.permutation(POOL)]
-        self.blocks: dict[str, list[int]] = {r: [] for r in prompts}
-        self.length: dict[str, int] = {r: 0 for r in prompts}
-        self.generation: dict[str, int] = {r: 0 for r in prompts}
-        self.ident = {r: i + 1 for i, r in enumerate(prompts)}
-        self.cache = np.zeros((POOL, BLOCK), dtype=np.int64)
+        self.pool = [int(b) for b in self.rng.permutation(pool_blocks)]
+        self.blocks: dict[str, list[int]] = {}
+        self.length: dict[str, int] = {}
+        self.generation: dict[str, int] = {}
+        self.ident: dict[str, int] = {}
+        self.cache = np.zeros((pool_blocks, BLOCK), dtype=np.int64)
         for r, n in prompts.items():
-            self.append(r, n)
+            self.admit(r, n)
+
+    def admit(self, r: str, n: int) -> None:
+        """A new request, prefilled with n tokens."""
+        self.blocks[r], self.length[r], self.generation[r] = [], 0, 0
+        self.ident[r] = len(self.ident) + 1
+        self.append(r, n)
 
     def value(self, r: str, t: int) -> int:
         return (self.ident[r] << 40) | (self.generation[r] << 32) | (t + 1)
+
+    def on_token(self, b: int, offset: int, r: str, t: int) -> None:
+        self.cache[b, offset] = self.value(r, t)
 
     def append(self, r: str, n: int) -> set[int]:
         """Write n more tokens of r; returns the blocks written."""
@@ -46,7 +56,7 @@ class Batch:
             if t % BLOCK == 0:
                 self.blocks[r].append(self.pool.pop())
             b = self.blocks[r][t // BLOCK]
-            self.cache[b, t % BLOCK] = self.value(r, t)
+            self.on_token(b, t % BLOCK, r, t)
             self.length[r] = t + 1
             touched.add(b)
         return touched
@@ -68,7 +78,7 @@ class Batch:
 
     def finish(self, r: str) -> None:
         self.release(r)
-        del self.blocks[r], self.length[r], self.generation[r]
+        del self.blocks[r], self.length[r], self.generation[r], self.ident[r]
 
     def in_use(self) -> list[int]:
         return sorted(b for bs in self.blocks.values() for b in bs)
