@@ -108,6 +108,42 @@ def pinned_copy_gbs(nbytes, to_host, repeats=5):
     return nbytes / (sum(per) / len(per)) / 1e6
 
 
+_SETTLE = {"probe": None, "idle_ms": None, "waited_s": 0.0}
+
+
+def settle_device(ext):
+    """Return torch's cached device memory to the driver, then wait until the copy engines are
+    free again before the next leg times anything. The driver clears released device memory in
+    the background on a copy engine: after 48 GiB was released, a pitched device-to-host copy ran
+    at 15 GB/s for about a second, where it runs at 56 GB/s otherwise. The wait ends when a probe
+    copy (32 MiB, pitched) runs within 25 % of its time on the idle device, or after 10 s; the
+    time waited is reported (``extra.settle_s``)."""
+    import torch
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    if _SETTLE["probe"] is None:  # made once, at the first call, on the idle device
+        _SETTLE["probe"] = (torch.empty(64 << 20, dtype=torch.uint8, device=dev),
+                            torch.empty(64 << 20, dtype=torch.uint8, pin_memory=True))
+    d, h = _SETTLE["probe"]
+
+    def probe_ms():
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        ext.copy_rows_async(h.data_ptr(), d.data_ptr(), 64, 512 << 10, 1 << 20, dev)
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e3
+
+    if _SETTLE["idle_ms"] is None:
+        probe_ms()
+        _SETTLE["idle_ms"] = min(probe_ms() for _ in range(3))
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < 10.0 and probe_ms() > 1.25 * _SETTLE["idle_ms"]:
+        time.sleep(0.05)
+    _SETTLE["waited_s"] += time.perf_counter() - t0
+
+
 def pmc_traffic():
     """HBM bytes per launch from the committed rocprofv3 counter profile (its latest
     measurement: the last traffic line), or None."""
@@ -160,7 +196,7 @@ def bench_c2(ext, steps, warmup, blocks_too=True):
         res["blocks_equal"] = bool(torch.equal(out.view(torch.int16), out2.view(torch.int16)))
         del out2
     del layers, out
-    torch.cuda.empty_cache()
+    settle_device(ext)
     return res
 
 
@@ -304,8 +340,12 @@ def bench_c2_layouts(ext, steps, warmup):
     rows = torch.empty((L, H, n, 2, D), dtype=torch.bfloat16, device=dev)
     algo = 2 * L * H * n * 2 * D * 2
     out = {}
+    # one allocation, viewed in each layout in turn: nothing is released between layouts
+    layer_elems = 2 * NB * BS * H * D
+    flat = torch.empty(L * layer_elems, dtype=torch.bfloat16, device=dev)
     for name, shape in shapes.items():
-        layers = [torch.empty(shape, dtype=torch.bfloat16, device=dev).normal_() for _ in range(L)]
+        layers = [flat[i * layer_elems:(i + 1) * layer_elems].view(shape).normal_()
+                  for i in range(L)]
         ptrs = torch.tensor([t.data_ptr() for t in layers], dtype=torch.long, device=dev)
         strides = layout_strides(layers[0])
         g, w = [], []
@@ -319,7 +359,8 @@ def bench_c2_layouts(ext, steps, warmup):
         out[name] = {"strides": list(strides), "gather_gbs": round(sorted(g)[1], 1),
                      "scatter_gbs": round(sorted(w)[1], 1)}
         del layers
-        torch.cuda.empty_cache()
+    del flat, rows
+    settle_device(ext)
     return out
 
 
@@ -427,7 +468,7 @@ def bench_c3(ext, steps, warmup):
     delivery = c3_file_delivery(ext, staging, L * H, n * row_bytes, dev)
     delivery["stager_round"] = c3_stager_round(ext, layers, blocks, dev)
     del layers, staging
-    torch.cuda.empty_cache()
+    settle_device(ext)
     plain = pinned_copy_gbs(payload, to_host=True)
     for k in ("deliver_gbs", "deliver_16_threads_gbs", "deliver_from_own_thread_gbs",
               "pageable_copy_gbs"):
@@ -485,6 +526,7 @@ def c3_file_delivery(ext, staging, runs, run_bytes, dev, repeats=5):
     addr = view.ctypes.data
     out = {"file": str(path.parent), "bounce_bytes": bounce_bytes,
            "host": {"cpu_count": os.cpu_count(), "affinity_cpus": len(os.sched_getaffinity(0)),
+                    "affinity": sorted(os.sched_getaffinity(0)), "numa": host_numa(),
                     "threading_env": {k: v for k, v in sorted(os.environ.items())
                                       if k.startswith(("OMP_", "GOMP_", "KMP_", "MKL_"))}}}
 
@@ -525,6 +567,19 @@ def c3_file_delivery(ext, staging, runs, run_bytes, dev, repeats=5):
                                        addr + at, per, 8)
 
         timed(host_half, "host_copy_only")
+
+        # the copy-engine half alone: the same batches into the two bounce buffers in turn
+        def dma_half():
+            with torch.cuda.stream(side):
+                for k, at in enumerate(range(0, payload - bounce_bytes + 1, bounce_bytes)):
+                    ext.copy_rows_async(bounce[k & 1].data_ptr(), staging.data_ptr() + at, 1,
+                                        bounce_bytes, bounce_bytes, dev)
+            side.synchronize()
+
+        timed(dma_half, "copy_engine_only")
+        out["host"]["bounce_numa_nodes"] = page_nodes([b.data_ptr() for b in bounce], bounce_bytes)
+        out["host"]["file_numa_nodes"] = page_nodes([addr], payload)
+        out["host"]["main_thread_cpu"] = current_cpu()
         sample = np.r_[0:1 << 20, payload - (1 << 20):payload]
         deliver(8)
         out["bytes_equal"] = bool(np.array_equal(view[sample],
@@ -538,6 +593,52 @@ def c3_file_delivery(ext, staging, runs, run_bytes, dev, repeats=5):
         del view
         mapping.close()
         path.unlink(missing_ok=True)
+    return out
+
+
+def page_nodes(ptrs, nbytes, every=1 << 20):
+    """The NUMA nodes of host pages, sampled every MiB of each buffer (move_pages, which only
+    reports), as {node: pages}; None where the call is unavailable."""
+    import ctypes
+
+    try:
+        libc = ctypes.CDLL(None, use_errno=True)
+        pages = [p + off for p in ptrs for off in range(0, nbytes, every)]
+        arr = (ctypes.c_void_p * len(pages))(*pages)
+        status = (ctypes.c_int * len(pages))()
+        if libc.syscall(279, 0, ctypes.c_ulong(len(pages)), arr, None, status, 0) != 0:
+            return None
+        counts = {}
+        for st in status:
+            counts[str(st)] = counts.get(str(st), 0) + 1
+        return counts
+    except (OSError, AttributeError):
+        return None
+
+
+def current_cpu():
+    import ctypes
+
+    try:
+        return int(ctypes.CDLL(None).sched_getcpu())
+    except (OSError, AttributeError):
+        return None
+
+
+def host_numa():
+    """The host's NUMA nodes with their CPUs, and the GPU's node, as sysfs reports them."""
+    out = {}
+    base = Path("/sys/devices/system/node")
+    for node in sorted(base.glob("node[0-9]*")) if base.is_dir() else []:
+        try:
+            out[node.name] = (node / "cpulist").read_text().strip()
+        except OSError:
+            pass
+    for card in sorted(Path("/sys/class/drm").glob("card[0-9]*/device/numa_node")):
+        try:
+            out[f"{card.parent.parent.name}_numa_node"] = card.read_text().strip()
+        except OSError:
+            pass
     return out
 
 
@@ -559,10 +660,12 @@ def c3_stager_round(ext, layers, blocks, dev):
             n = st.commit_blocks(1, k + 1, blocks.tolist())
             st.flush()
             times.append(time.perf_counter() - t0)
+        bounce_nodes = page_nodes([b.data_ptr() for b in st._bounce], st._bounce_bytes)
     payload = n * len(layers) * layers[0].shape[-1] * 2
     ms = sorted(times[1:])[0] * 1e3
     return {"first_ms": round(times[0] * 1e3, 3), "ms": round(ms, 3),
-            "gbs": round(payload / ms / 1e6, 2)}
+            "gbs": round(payload / ms / 1e6, 2), "repeats_ms": [round(t * 1e3, 2) for t in times],
+            "bounce_numa_nodes": bounce_nodes}
 
 
 # ------------------------------------------------------------------------------ C4 restore
@@ -645,7 +748,7 @@ def bench_c4(ext, steps, warmup):
     torch.cuda.synchronize()
     ok_r = bool(torch.equal(back.view(torch.int16), rows[:4].view(torch.int16)))
     del rows, caches, back
-    torch.cuda.empty_cache()
+    settle_device(ext)
     ms = sum(per) / len(per)
     ms_o = sum(per_o) / len(per_o)
     ms_d = sum(per_d) / len(per_d)
@@ -791,7 +894,7 @@ def bench_restore_host(ext, steps, warmup):
     finally:
         shutil.rmtree(tmp, ignore_errors=True)
     del caches
-    torch.cuda.empty_cache()
+    settle_device(ext)
     plain = pinned_copy_gbs(1 << 30, to_host=False)
     return {
         "config": f"restore of {L * H} store tables of C4 shape ([262144, 2, 128] bf16, 128 MiB "
@@ -913,6 +1016,17 @@ def bench_restore_catch_up(ext, steps, warmup):
                 release_later(tables).join()
                 release.append(time.perf_counter() - t0)
             launches = restorer.timing.get("launches")
+            # a spare that keeps the tables mapped from its first restore to the swap: the
+            # catch-up then opens nothing and faults no page in
+            kept = [Table.open(t, p, written) for t, p in paths.items()]
+            restorer.restore(kept, head_map)
+            mapped = []
+            for _ in range(3):
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                restorer.restore(kept, head_map)
+                mapped.append(time.perf_counter() - t0)
+            release_later(kept).join()
             # check two tables' rows in their new head slots
             ok = got == rows_per_table * L * H
             s_dev = torch.from_numpy(slots).to(dev)
@@ -963,10 +1077,11 @@ def bench_restore_catch_up(ext, steps, warmup):
             "first_speedup": round(ref[0] / ours[0], 2),
             "scatter_launches": launches,
             "ours_parts_ms": parts,
+            "ours_tables_kept_mapped_ms": round(sorted(mapped)[1] * 1e3, 3),
             "rows_check": bool(ok),
         }
     del caches, restorer
-    torch.cuda.empty_cache()
+    settle_device(ext)
     return out
 
 
@@ -1092,7 +1207,7 @@ def bench_c5(ext, steps, warmup):
     st = int(state[0].item())
     flags[3] = 1
     del sets
-    torch.cuda.empty_cache()
+    settle_device(ext)
     decode = reduce_decode_sizes(ext, flags, order, state, steps, dev)
     late = reduce_late_member(ext, dev)
     us = sum(per) / len(per) * 1e3
@@ -1417,7 +1532,7 @@ def bench_decode_overhead(ext, steps, warmup):
     # the batch-32 step reads half the K and V
     step8_32_bytes = step8_bytes - Lyr * (B - B32) * HKV * CTX * DH * 2 * 2
     del w, w8, cache, graph, graph8, graph8_32
-    torch.cuda.empty_cache()
+    settle_device(ext)
     return {
         "config": "Llama-3-8B decode-step proxy: 32 layers, batch 64, ctx 1024, bf16 (nn.Linear "
                   "layout GEMMs, SDPA per KV head), the forward in one HIP graph, the host "
@@ -1696,6 +1811,7 @@ def main(argv=None):
         pcie_workload(ext)
         return 0
     log(f"device {torch.cuda.get_device_name(0)}; library {ext.__file__}")
+    settle_device(ext)  # the copy probe's idle time, on the device before any leg allocates
 
     c2 = bench_c2(ext, a.steps, a.warmup, blocks_too=not a.quick)
     per = c2["per_launch_ms"]
@@ -1759,6 +1875,7 @@ def main(argv=None):
         if not a.quick and not wanted:
             log("cpu baselines of the restore and the reduce ...")
             result["extra"]["cpu_baselines_more"] = cpu_baselines_more()
+    result["extra"]["settle_s"] = round(_SETTLE["waited_s"], 3)
     if failed:
         result["extra"]["failed_legs"] = failed
     wrong = failed_checks(result)

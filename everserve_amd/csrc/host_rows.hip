@@ -229,12 +229,10 @@ int deliver(char* dst, int64_t dst_pitch, const char* src, int64_t src_pitch, in
   split_last(batches);
   auto issue = [&](size_t i) -> int {
     const Batch& b = batches[i];
-    // one run has no pitch of its own: give the copy its width (the caller's may be smaller)
-    const size_t spitch = static_cast<size_t>(b.nruns > 1 ? src_pitch : b.len);
-    EVS_HIP(hipMemcpy2DAsync(bounce[i & 1], static_cast<size_t>(b.len),
-                             src + b.run0 * src_pitch + b.offset, spitch,
-                             static_cast<size_t>(b.len), static_cast<size_t>(b.nruns),
-                             hipMemcpyDeviceToHost, stream));
+    const int rc = copy_runs(bounce[i & 1], b.len, src + b.run0 * src_pitch + b.offset,
+                             b.nruns > 1 ? src_pitch : b.len, b.len, b.nruns,
+                             hipMemcpyDeviceToHost, stream);
+    if (rc != EVS_OK) return rc;
     EVS_HIP(hipEventRecord(ev[i & 1], stream));
     return EVS_OK;
   };

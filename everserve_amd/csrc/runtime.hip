@@ -165,15 +165,8 @@ extern "C" int evs_copy_rows_async(void* dst, const void* src, int64_t groups, i
               "evs_copy_rows_async: needs groups >= 0 and pitch >= bytes >= 0");
   if (groups == 0 || bytes == 0) return EVS_OK;
   EVS_REQUIRE(dst != nullptr && src != nullptr, "evs_copy_rows_async: null pointer");
-  if (bytes == pitch || groups == 1) {
-    EVS_HIP(hipMemcpyAsync(dst, src, static_cast<size_t>((groups - 1) * pitch + bytes),
-                           hipMemcpyDefault, evs::as_stream(stream)));
-  } else {
-    EVS_HIP(hipMemcpy2DAsync(dst, static_cast<size_t>(pitch), src, static_cast<size_t>(pitch),
-                             static_cast<size_t>(bytes), static_cast<size_t>(groups),
-                             hipMemcpyDefault, evs::as_stream(stream)));
-  }
-  return EVS_OK;
+  return evs::copy_runs(dst, pitch, src, pitch, bytes, groups, hipMemcpyDefault,
+                        evs::as_stream(stream));
 }
 
 extern "C" int evs_event_create(int system_fence, void** event) {
