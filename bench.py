@@ -696,6 +696,18 @@ def bench_c4(ext, steps, warmup):
     torch.cuda.synchronize()
     ok = bool(torch.equal(back.view(torch.int16), rows[:4].view(torch.int16)))
 
+    # the same call with its sorting turned off: the writes in staged order
+    before = ext.scatter_rows_ordering(-1, -1)
+    try:
+        for t in caches[:4]:
+            t.zero_()
+        per_s, _ = time_launches(scatter, steps, warmup, stream)
+        ext.gather_rows(ptrs[:4], s, heads, back.data_ptr(), n, D, BS, strides, 2)
+        torch.cuda.synchronize()
+        ok_s = bool(torch.equal(back.view(torch.int16), rows[:4].view(torch.int16)))
+    finally:
+        ext.scatter_rows_ordering(*before)
+
     # the same restore with its writes in cache order: the (slot, staged row) pairs sorted by slot
     # on the host from the block table, then scatter_pairs
     from everserve_amd.state.restore import destination_order
@@ -750,19 +762,30 @@ def bench_c4(ext, steps, warmup):
     del rows, caches, back
     settle_device(ext)
     ms = sum(per) / len(per)
+    ms_s = sum(per_s) / len(per_s)
     ms_o = sum(per_o) / len(per_o)
     ms_d = sum(per_d) / len(per_d)
     ms_r = sum(per_r) / len(per_r)
     return {
         "config": "C4 restore: [32,8,262144,2,128] bf16 rows into a fresh 16384-block cache, "
                   "random-permutation block table (64 seqs x 4096 tokens)",
-        "paths": "scatter_* here: evs_scatter_rows with the rows in staged order; the Restorer "
-                 "(a restore from the store's tables) launches evs_scatter_ranges, measured in "
-                 "by_ranges_in_slot_order",
+        "paths": "scatter_* here: evs_scatter_rows as built, which at this size sorts its "
+                 "(slot, row) pairs by slot on the device and writes them through the pair "
+                 "scatter (the sort inside each timed call); staged_order: the same call with "
+                 "the sorting off; the Restorer (a restore from the store's tables) launches "
+                 "evs_scatter_ranges, measured in by_ranges_in_slot_order",
         "scatter_ms": round(ms, 3),
         "scatter_gbs": round(2 * payload / ms / 1e6, 1),
         "scatter_frac_of_8tbs": round(2 * payload / ms / 1e6 / PEAK_HBM_GBS, 4),
         "round_trip_equal_first_4_layers": ok,
+        "staged_order": {
+            "how": "evs_scatter_rows with evs_scatter_rows_ordering(-1, -1): one kernel, the "
+                   "rows read in staged order, each half-row written at its slot",
+            "scatter_ms": round(ms_s, 3),
+            "scatter_gbs": round(2 * payload / ms_s / 1e6, 1),
+            "scatter_frac_of_8tbs": round(2 * payload / ms_s / 1e6 / PEAK_HBM_GBS, 4),
+            "round_trip_equal_first_4_layers": ok_s,
+        },
         "ordered": {
             "how": "scatter_pairs with the pairs in slot order (destination_order on the host: "
                    "the block table's 16,384 blocks sorted)",

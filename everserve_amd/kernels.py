@@ -186,6 +186,7 @@ _SIGNATURES: tuple[tuple[str, object, tuple], ...] = (
         (_P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _P, _I64, _P, _P),
     ),
     ("evs_scatter_rows", _I32, (_P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _P, _I64, _P)),
+    ("evs_scatter_rows_ordering", _I32, (_I64, _I64, _P)),
     ("evs_scatter_pairs", _I32,
      (_P, _I64, _P, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _P, _I64, _P)),
     ("evs_scatter_ranges", _I32,
@@ -412,6 +413,14 @@ class Kernels:
                     _stream_of(slots.device),
                 )
             )
+
+    def scatter_rows_ordering(self, min_rows: int, min_bytes: int) -> tuple[int, int]:
+        """Set the sizes from which :meth:`scatter_rows` sorts its pairs by slot before writing
+        (at least ``min_rows`` slots and ``min_bytes`` of rows; negative: never); returns the
+        values in force before. Process-wide."""
+        prev = (ctypes.c_int64 * 2)()
+        self._check(self._lib.evs_scatter_rows_ordering(int(min_rows), int(min_bytes), prev))
+        return int(prev[0]), int(prev[1])
 
     def scatter_pairs(
         self,

@@ -75,10 +75,29 @@ def test_block_gather_equals_the_gather_of_the_expanded_slots(ext, layout, d):
     assert tags.cpu().tolist() == slots.tolist()
 
 
+@pytest.fixture
+def sorted_first(ext):
+    """scatter_rows sorting its pairs by slot at every size, for the test's length."""
+    before = ext.scatter_rows_ordering(0, 0)
+    yield
+    ext.scatter_rows_ordering(*before)
+
+
+@pytest.fixture
+def staged_only(ext):
+    """scatter_rows writing in staged order at every size, for the test's length."""
+    before = ext.scatter_rows_ordering(-1, -1)
+    yield
+    ext.scatter_rows_ordering(*before)
+
+
+@pytest.mark.parametrize("order", ["as built", "sorted first"])
 @pytest.mark.parametrize("layout", LAYOUTS)
 @pytest.mark.parametrize("d", [8, 6])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float8_e4m3fn])
-def test_scatter_writes_exactly_what_the_oracle_writes(ext, layout, d, dtype):
+def test_scatter_writes_exactly_what_the_oracle_writes(ext, request, order, layout, d, dtype):
+    if order == "sorted first":
+        request.getfixturevalue("sorted_first")
     src = caches(layout, d, dtype, seed=5)
     dst = caches(layout, d, dtype, seed=9)  # a cache that already holds other rows
     _, _, bs, _ = oracle.recognise(src[0].shape)
@@ -141,6 +160,75 @@ def test_a_captured_gather_replays_like_an_eager_call(ext):
                                               bits(torch.full((1,), float(i), dtype=torch.bfloat16))[0],
                                               dtype=np.uint16))
         assert np.array_equal(bits(out), want), i
+
+
+def test_a_captured_scatter_writes_in_staged_order_and_replays_right(ext, sorted_first):
+    """Under graph capture scatter_rows does not sort (the sort clears its counters with a memset,
+    which a captured graph must not hold), whatever its thresholds: the graph holds the staged
+    order's one kernel, and each replay writes what the oracle writes, the slot ids changed in
+    place between replays and the cache reset by eager work."""
+    src = caches("kv_first", 8, torch.bfloat16, seed=5)
+    base = caches("kv_first", 8, torch.bfloat16, seed=9)
+    staged = oracle.gather_rows(src, SLOTS, HEADS, CAPACITY, 8, 4, strides_of(src[0]), 2)
+    rows = torch.from_numpy(staged.copy()).cuda()
+    gpu = [t.cuda() for t in base]
+    table = ptrs(gpu)
+    s = torch.tensor(SLOTS, dtype=torch.long, device="cuda")
+    h = torch.tensor([2, 0], dtype=torch.long, device="cuda")
+    strides = list(strides_of(gpu[0]))
+    side = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        ext.scatter_rows(table, s, h, rows.data_ptr(), CAPACITY, 8, 4, strides, 2)
+    for i, slots in enumerate([SLOTS, [27, 3, -1, 9, 0], SLOTS[::-1]]):
+        s.copy_(torch.tensor(slots))
+        for g, b in zip(gpu, base):
+            g.copy_(b)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        want = [t.clone() for t in base]
+        oracle.scatter_rows(want, slots, [2, 0], staged, CAPACITY, 8, 4, strides_of(base[0]), 2)
+        for got, w in zip(gpu, want):
+            assert np.array_equal(bits(got), bits(w)), i
+
+
+def test_sorted_calls_on_two_streams_take_turns_with_the_workspace(ext, sorted_first):
+    """Two sorting scatters enqueued back to back on two streams, with no synchronisation between
+    them, share the library's workspace: the second waits for the first's scatter before its sort
+    writes the workspace again. Each cache ends as the oracle writes it; the second call's slots
+    are twice as many, so the workspace also grows between two calls in flight."""
+    L, NB, BS, H, D = 4, 256, 16, 4, 64
+    rng = np.random.default_rng(61)
+    shape = (2, NB, BS, H, D)
+    jobs = []
+    for k, n in enumerate((1024, 4096)):
+        slots = rng.permutation(NB * BS)[:n].astype(np.int64)
+        slots[rng.integers(0, n, 8)] = -1  # padding, skipped by either order
+        staged = torch.randn((L, H, n, 2, D), generator=torch.Generator().manual_seed(70 + k))
+        staged = staged.to(torch.bfloat16)
+        base = [torch.randn(shape, generator=torch.Generator().manual_seed(80 + 10 * k + i))
+                .to(torch.bfloat16) for i in range(L)]
+        jobs.append((slots, staged, base, [t.cuda() for t in base]))
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    keep = []
+    for (slots, staged, _, gpu), stream in zip(jobs, streams):
+        with torch.cuda.stream(stream):
+            s = torch.from_numpy(slots).cuda()
+            rows = staged.cuda()
+            h = torch.arange(H, dtype=torch.long, device="cuda")
+            table = ptrs(gpu)
+            keep += [s, rows, h, table]
+            ext.scatter_rows(table, s, h, rows.data_ptr(), len(slots), D, BS,
+                             list(strides_of(gpu[0])), 2)
+    torch.cuda.synchronize()
+    for slots, staged, base, gpu in jobs:
+        want = [t.clone() for t in base]
+        oracle.scatter_rows(want, slots, list(range(H)), bits(staged), len(slots), D, BS,
+                            strides_of(base[0]), 2)
+        for got, w in zip(gpu, want):
+            assert np.array_equal(bits(got), bits(w))
 
 
 # ----------------------------------------------------------------- the configs' shapes
@@ -281,7 +369,8 @@ def test_copy_rows_moves_only_the_filled_rows(ext):
 def test_c4_restore_round_trip_full_size(ext):
     """C4: 64 seqs x 4096 tokens of Llama-3-8B rows (32 GiB) scattered into a fresh
     16384-block cache through a seeded random-permutation block table, gathered back: equal,
-    through both scatters."""
+    three ways: scatter_rows as built (at this size it sorts its pairs on the device first),
+    scatter_rows in staged order, and scatter_pairs with the pairs sorted on the host."""
     L, NB, BS, H, D = 32, 16384, 16, 8, 128
     n = NB * BS
     rows = torch.empty((L, H, n, 2, D), dtype=torch.bfloat16, device="cuda")
@@ -292,14 +381,19 @@ def test_c4_restore_round_trip_full_size(ext):
     heads = torch.arange(H, dtype=torch.long, device="cuda")
     strides = list(strides_of(cache[0]))
     back = torch.empty((8, H, n, 2, D), dtype=torch.bfloat16, device="cuda")
-    # in staged order (scatter_rows), then the same restore in cache order (scatter_pairs with
-    # the pairs destination_order sorts from the block table), each into zeroed caches
+    # each into zeroed caches; the host's order is destination_order's, from the block table
     sorted_slots, rows_of = destination_order(slots, block_size=BS)
-    for how in ("staged order", "cache order"):
+    for how in ("as built", "staged order", "cache order"):
         for t in cache:
             t.zero_()
-        if how == "staged order":
+        if how == "as built":
             ext.scatter_rows(ptrs(cache), s, heads, rows.data_ptr(), n, D, BS, strides, 2)
+        elif how == "staged order":
+            before = ext.scatter_rows_ordering(-1, -1)
+            try:
+                ext.scatter_rows(ptrs(cache), s, heads, rows.data_ptr(), n, D, BS, strides, 2)
+            finally:
+                ext.scatter_rows_ordering(*before)
         else:
             ext.scatter_pairs(ptrs(cache), torch.from_numpy(sorted_slots).cuda(),
                               torch.from_numpy(rows_of).cuda(), heads, rows.data_ptr(), n, D, BS,
