@@ -1702,8 +1702,10 @@ def pmc_workload(ext, which="gather", launches=5):
     FETCH_SIZE and WRITE_SIZE are known to be 1 GiB each, the scale the kernel's counters are
     read against.
 
-    gather: the C2 gather. scatter: the C4 restore scatter (32 layers, 64 GiB moved). pairs: the
-    same restore in cache order (scatter_pairs, the pairs sorted by slot). ranges: the same rows
+    gather: the C2 gather. scatter: the C4 restore scatter (32 layers, 64 GiB moved) through
+    scatter_rows as built (at this size: its pairs sorted on the device, then the pair scatter).
+    staged: the same call with the sorting off (one kernel, staged order). pairs: the same restore
+    in cache order (scatter_pairs, the pairs sorted by slot on the host). ranges: the same rows
     restored as one written range per layer, slots 0..n-1 in order (scatter_ranges, as the
     Restorer launches it, at C4's size). reduce: the C5 local
     reduce, each call on another of 32 buffer sets (1.1 GiB in all, over 4x what the Infinity
@@ -1728,7 +1730,7 @@ def pmc_workload(ext, which="gather", launches=5):
             ext.gather_rows(ptrs, s, heads, out.data_ptr(), n, D, BS, strides, 2)
         algo = 2 * L * H * n * 2 * D * 2
         del layers, out
-    elif which in ("scatter", "pairs", "ranges"):
+    elif which in ("scatter", "staged", "pairs", "ranges"):
         L, NB, BS, H, D = 32, 16384, 16, 8, 128
         n = NB * BS
         # the counters count bytes, whatever they hold: the rows are left uninitialised
@@ -1747,6 +1749,7 @@ def pmc_workload(ext, which="gather", launches=5):
             os_dev, or_dev = torch.from_numpy(o_slots).to(dev), torch.from_numpy(o_rows).to(dev)
         starts = torch.zeros(1, dtype=torch.long, device=dev)
         first_rows = torch.tensor([0, n], dtype=torch.long, device=dev)
+        before = ext.scatter_rows_ordering(-1, -1) if which == "staged" else None
         for _ in range(launches):
             if which == "ranges":
                 ext.scatter_ranges(ptrs, starts, first_rows, n, heads, rows.data_ptr(), n, D, BS,
@@ -1756,6 +1759,8 @@ def pmc_workload(ext, which="gather", launches=5):
                                   2)
             else:
                 ext.scatter_rows(ptrs, s, heads, rows.data_ptr(), n, D, BS, strides, 2)
+        if before is not None:
+            ext.scatter_rows_ordering(*before)
         algo = 2 * L * H * n * 2 * D * 2
         del rows, caches
     elif which == "reduce":
@@ -1800,7 +1805,7 @@ def main(argv=None):
                     help="only the host copies of the path beside plain copies, for a "
                          "rocprofv3 memory-copy trace")
     ap.add_argument("--pmc", nargs="?", const="gather", default=None,
-                    choices=("gather", "scatter", "pairs", "ranges", "reduce"),
+                    choices=("gather", "scatter", "staged", "pairs", "ranges", "reduce"),
                     help="only a counter run's workload: 5 calls of the named kernel (default "
                          "gather), then 5 calibration copies")
     a = ap.parse_args(argv)
