@@ -95,7 +95,8 @@ constexpr int64_t kMinRunCopyBytes = int64_t{1} << 20;
 // EVS_HOST_COPY_DMA 1 sends every host copy of explicit direction through hipMemcpy2DAsync, 2
 // those of hipMemcpyDefault too. Measured against the default on a Llama-3-8B decode step that
 // stages 8 MiB a step: the snapshot added 40-47 us a step either way (10 interleaved rounds of 100
-// steps), so the default stays, which is immune to the background clearing above.
+// steps), so the default stays: its contiguous copies and device-to-host runs of 1 MiB or more go
+// as blit kernels, which the background clearing above does not slow.
 #ifndef EVS_HOST_COPY_DMA
 #define EVS_HOST_COPY_DMA 0
 #endif
