@@ -101,7 +101,9 @@ int evs_gather_blocks(const int64_t* layer_ptrs, int64_t num_layers, const int32
  * the first such call on a device allocates a workspace of about 24 bytes a slot that the library
  * keeps (and grows) for later ones; calls on one device take turns with it, each waiting on its
  * own stream for the previous one. A call on a stream under graph capture, or one for which no
- * workspace can be had, writes in staged order. Replaces the restore's per-table
+ * workspace can be had, writes in staged order. The first such call allocates with hipMalloc,
+ * which a graph capture in global mode elsewhere in the process forbids: make it before such a
+ * capture starts, or turn the sorting off. Replaces the restore's per-table
  * PagedKV.write_rows scatter (core/everserve/state/mirror.py:926-937,
  * core/everserve/state/kvcopy.py:118-128). */
 int evs_scatter_rows(const int64_t* layer_ptrs, int64_t num_layers, const int64_t* slots,
