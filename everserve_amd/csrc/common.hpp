@@ -92,32 +92,17 @@ constexpr int64_t kMinRunCopyBytes = int64_t{1} << 20;
 // between HBM and pinned host memory, 32 KiB to 32 MiB either way, runs as a blit kernel on a
 // compute queue (8 MiB device-to-host: 151 us of kernel, 42-47 GB/s); hipMemcpy2DAsync, pitched
 // or not, even one row, runs on a DMA engine and launches no kernel (8 MiB: 161 us, 52 GB/s).
-// EVS_HOST_COPY_DMA 1 sends every host copy of explicit direction through hipMemcpy2DAsync, 2
-// those of hipMemcpyDefault too. Measured against the default on a Llama-3-8B decode step that
-// stages 8 MiB a step: the snapshot added 40-47 us a step either way (10 interleaved rounds of 100
-// steps), so the default stays: its contiguous copies and device-to-host runs of 1 MiB or more go
-// as blit kernels, which the background clearing above does not slow.
-#ifndef EVS_HOST_COPY_DMA
-#define EVS_HOST_COPY_DMA 0
-#endif
+// Sending every host copy through hipMemcpy2DAsync was measured against the forms below on a
+// Llama-3-8B decode step that stages 8 MiB a step: the snapshot added 40-47 us a step either way
+// (10 interleaved rounds of 100 steps). The forms below stay: their contiguous copies and
+// device-to-host runs of 1 MiB or more go as blit kernels, which the background clearing above
+// does not slow.
 
 inline int copy_runs(void* dst, int64_t dpitch, const void* src, int64_t spitch, int64_t len,
                      int64_t runs, hipMemcpyKind kind, hipStream_t stream) {
   if (runs <= 0 || len <= 0) return EVS_OK;
   char* d = static_cast<char*>(dst);
   const char* s = static_cast<const char*>(src);
-  if (EVS_HOST_COPY_DMA &&
-      (kind == hipMemcpyDeviceToHost || kind == hipMemcpyHostToDevice ||
-       (EVS_HOST_COPY_DMA > 1 && kind == hipMemcpyDefault))) {
-    if (runs == 1 || (dpitch == len && spitch == len)) {
-      const size_t all = static_cast<size_t>(len * runs);
-      EVS_HIP(hipMemcpy2DAsync(d, all, s, all, all, 1, kind, stream));
-    } else {
-      EVS_HIP(hipMemcpy2DAsync(d, static_cast<size_t>(dpitch), s, static_cast<size_t>(spitch),
-                               static_cast<size_t>(len), static_cast<size_t>(runs), kind, stream));
-    }
-    return EVS_OK;
-  }
   if (runs == 1 || (dpitch == len && spitch == len)) {
     EVS_HIP(hipMemcpyAsync(d, s, static_cast<size_t>(len * runs), kind, stream));
   } else if (kind == hipMemcpyDeviceToHost && len >= kMinRunCopyBytes) {
