@@ -315,19 +315,51 @@ __device__ __forceinline__ TileId tile_id(const RowsArgs& a, uint32_t b) {
 }
 
 // The slot of staged row t (0 <= t < n) in the written ranges: the last range k whose first row
-// is at most t, found by bisection over first_rows (ascending, first_rows[0] = 0, the last entry
-// n), so an empty range is passed over. Ranges that break these rules give slots the caller did
-// not mean, as wrong slot ids would; a negative one moves nothing.
-__device__ __forceinline__ int64_t slot_in_ranges(const RowsArgs& a, int64_t t) {
-  int64_t lo = 0, hi = a.nranges;
+// is at most t (first_rows ascending, first_rows[0] = 0, the last entry n), so an empty range is
+// passed over. Ranges that break these rules give slots the caller did not mean, as wrong slot ids
+// would; a negative one moves nothing. Found for a tile's rows by the tile's first wave together:
+// every lane of wave 0 calls it, lane i with row t = t0 + i (rows past the tile's repeat its last;
+// t0 <= t < n). The range
+// of t0 is found by a 64-way search, each level one read a lane and a ballot (two levels up to
+// 4,096 ranges, where bisection takes a dependent read for each of 12 halvings); then the 64
+// ranges from there are read at once, first rows and starts, and each lane picks its own among
+// them with shuffles. A lane whose row lies past those 64 ranges (only when many ranges are
+// empty) bisects the rest. Every read stays inside first_rows[0 .. nranges] and
+// starts[0 .. nranges - 1] whatever the arrays hold.
+__device__ __forceinline__ int64_t wave_slot_in_ranges(const RowsArgs& a, int64_t t0, int64_t t) {
+  const int64_t nr = a.nranges;
+  if (nr == 1) return a.starts[0] + (t - a.first_rows[0]);
+  const int lane = static_cast<int>(threadIdx.x & 63);
+  int64_t lo = 0, hi = nr;  // the range of t0 is in [lo, hi)
   while (hi - lo > 1) {
-    const int64_t mid = (lo + hi) >> 1;
-    if (a.first_rows[mid] <= t)
-      lo = mid;
-    else
-      hi = mid;
+    const int64_t step = (hi - lo + 63) >> 6;
+    const int64_t p = lo + lane * step;
+    const uint64_t le = __ballot(p < hi && a.first_rows[p] <= t0);
+    lo += le != 0 ? static_cast<int64_t>(63 - __builtin_clzll(le)) * step : 0;
+    hi = lo + step < hi ? lo + step : hi;
   }
-  return a.starts[lo] + (t - a.first_rows[lo]);
+  const int64_t k = lo + lane;
+  const int64_t fr = a.first_rows[k < nr ? k : nr];  // first_rows[nr] = n: past every row
+  const int64_t st = a.starts[k < nr ? k : nr - 1];
+  // c: the last of the 64 whose first row is at most t
+  int c = 0;
+  for (int b = 32; b >= 1; b >>= 1) {
+    const int64_t v = __shfl(fr, c + b);
+    if (v <= t) c += b;
+  }
+  int64_t slot = __shfl(st, c) + (t - __shfl(fr, c));
+  if (c == 63 && lo + 63 < nr - 1) {
+    int64_t l2 = lo + 63, h2 = nr;
+    while (h2 - l2 > 1) {
+      const int64_t mid = (l2 + h2) >> 1;
+      if (a.first_rows[mid] <= t)
+        l2 = mid;
+      else
+        h2 = mid;
+    }
+    slot = a.starts[l2] + (t - a.first_rows[l2]);
+  }
+  return slot;
 }
 
 // The index entry row t of a layer needs: its slot id, or in the block-table path its block's id.
@@ -337,7 +369,6 @@ template <int I>
 __device__ __forceinline__ int64_t index_entry(const RowsArgs& a, int64_t t) {
   const int64_t tc = t < a.n ? t : a.n - 1;
   if (I == kByBlocks) return a.blocks[block_of(tc, a)];
-  if (I == kByRanges) return slot_in_ranges(a, tc);
   return a.slots[tc];
 }
 
@@ -452,9 +483,15 @@ __device__ __forceinline__ void tile_offsets(const RowsArgs& a, const TileId& id
                                              int64_t* s_slot, int64_t* s_head, int64_t* s_src) {
   const int tid = threadIdx.x;
   const int h0 = static_cast<int>(id.group) * a.HG;
+  static_assert(kMaxTileSlots == 64, "the first wave fills a tile's slots: one lane a slot");
   if (tid < kMaxTileSlots) {
     const int64_t t = t0 + (tid < a.TS ? tid : a.TS - 1);
-    const int64_t entry = index_entry<I == kByPairs ? kBySlots : I>(a, t);  // a slot, or a block
+    // a slot, or a block; the range path reads as a wave, the others a lane at a time
+    int64_t entry;
+    if constexpr (I == kByRanges)
+      entry = wave_slot_in_ranges(a, t0, t < a.n ? t : a.n - 1);
+    else
+      entry = index_entry<I == kByPairs ? kBySlots : I>(a, t);
     const int64_t src = I == kByPairs ? a.rows_of[t < a.n ? t : a.n - 1] : 0;
     const int hc = h0 + (tid < a.HG ? tid : a.HG - 1);
     const int64_t head = a.heads[hc < a.H ? hc : a.H - 1];

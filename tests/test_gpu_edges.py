@@ -369,6 +369,54 @@ def test_scatter_ranges_over_several_layers_and_nothing_to_move(ext):
                            dev_long([0]), r.data_ptr(), cap, 8, BS, list(strides_of(gpu[0])), 2)
 
 
+def range_cases():
+    """(name, starts, counts) over a 16,384-slot cache: more ranges than two levels of the
+    kernel's 64-way search reach (4,096), runs of empty ranges longer than the 64 ranges a tile
+    reads ahead (a row past them is found by bisection), empty ranges first, and 2 and 65 ranges."""
+    rng = np.random.default_rng(71)
+    out = []
+    counts = rng.integers(0, 4, 5000)  # 5,000 ranges of 0-3 rows, gaps of 0-1 slots between
+    gaps = rng.integers(0, 2, 5000)
+    starts = np.cumsum(np.concatenate(([0], (counts + gaps)[:-1])))
+    out.append(("5000 ranges", starts, counts))
+    starts = [5, 40] + [100] * 300 + [200, 900] + [1000] * 70 + [3000]
+    counts = [3, 50] + [0] * 300 + [1, 64] + [0] * 70 + [90]
+    out.append(("runs of empty ranges", np.array(starts), np.array(counts)))
+    starts = [7] * 10 + [50, 16000]
+    counts = [0] * 10 + [30, 384]
+    out.append(("empty ranges first", np.array(starts), np.array(counts)))
+    out.append(("2 ranges", np.array([900, 10]), np.array([70, 5])))
+    out.append(("65 ranges", np.arange(65) * 250, np.full(65, 3)))
+    return out
+
+
+@pytest.mark.parametrize("case", range(5))
+def test_scatter_ranges_through_many_ranges_and_runs_of_empty_ones(ext, case):
+    """Each row's range is found by the tile's first wave together (a 64-way search, then 64
+    ranges read ahead); these cases reach every part of that: a third search level, rows past the
+    64 ranges read ahead, leading empty ranges. Equal to the oracle's slot scatter at the
+    expanded slots, 64-row tiles (bf16, d = 8)."""
+    name, starts, counts = range_cases()[case]
+    nb, bs, h, d = 1024, 16, 2, 8
+    slots = np.concatenate([np.arange(a, a + k, dtype=np.int64) for a, k in zip(starts, counts)])
+    assert slots.max() < nb * bs and len(slots) == len(np.unique(slots)), name
+    n = len(slots)
+    first_rows = np.concatenate(([0], np.cumsum(counts))).astype(np.int64)
+    src = caches("kv_first", d, torch.bfloat16, n_layers=2, nb=nb, bs=bs, h=h, seed=72)
+    rows = oracle.gather_rows(src, np.arange(n) % (nb * bs), [0, 1], n, d, bs,
+                              strides_of(src[0]), 2)
+    dst = caches("kv_first", d, torch.bfloat16, n_layers=2, nb=nb, bs=bs, h=h, seed=73)
+    want = [t.clone() for t in dst]
+    oracle.scatter_rows(want, slots, [1, 0], rows, n, d, bs, strides_of(want[0]), 2)
+    gpu = [t.cuda() for t in dst]
+    r = torch.from_numpy(rows.view(np.int16).copy()).cuda()
+    ext.scatter_ranges(ptrs(gpu), dev_long(starts), dev_long(first_rows), n, dev_long([1, 0]),
+                       r.data_ptr(), n, d, bs, list(strides_of(gpu[0])), 2)
+    torch.cuda.synchronize()
+    for g, w in zip(gpu, want):
+        assert np.array_equal(bits(g), bits(w)), name
+
+
 @pytest.mark.parametrize("layout", LAYOUTS)
 def test_a_bound_gather_writes_what_gather_rows_writes(ext, layout):
     """Kernels.bind_gather (the step path's launcher, its fixed arguments checked once) against
