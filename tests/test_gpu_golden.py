@@ -44,8 +44,20 @@ def test_the_gather_writes_the_stored_rows(ext, case):
     assert np.array_equal(out.cpu().numpy().view(want.dtype).reshape(want.shape), want)
 
 
+@pytest.mark.parametrize("sort", [False, True])
 @pytest.mark.parametrize("case", [c for c in CASES if c.endswith("bf16")])
-def test_the_scatter_writes_the_stored_caches(ext, case):
+def test_the_scatter_writes_the_stored_caches(ext, case, sort):
+    """scatter_rows as it runs at these sizes (staged order), and with its pairs sorted by slot
+    first, as it runs from 2^18 slots and 8 GiB (the thresholds lowered to zero)."""
+    before = ext.scatter_rows_ordering(0, 0) if sort else None
+    try:
+        scatter_and_check(ext, case)
+    finally:
+        if before is not None:
+            ext.scatter_rows_ordering(*before)
+
+
+def scatter_and_check(ext, case):
     layers = [torch.zeros_like(t).cuda() for t in tensors(case)]
     rows = torch.from_numpy(G[f"{case}_rows"].view(np.int16).copy()).cuda()
     d = int(case.rsplit("_", 2)[1][1:])
