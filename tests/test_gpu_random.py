@@ -8,6 +8,8 @@ The gather writes into a buffer filled with a sentinel, so the rows past n must 
 scatters write into caches of random content, compared whole (the head a view leaves out too).
 """
 
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -17,7 +19,8 @@ from tests.cases import NP_BITS, TORCH_BITS, bits, random_case, strides_of
 
 pytestmark = pytest.mark.gpu
 
-SEEDS = range(40)
+# EVERSERVE_RANDOM_CASES widens the sweep for a longer run; 40 by default
+SEEDS = range(int(os.environ.get("EVERSERVE_RANDOM_CASES", "40")))
 SENTINEL = {1: 0x5A, 2: 0x5A5A, 4: 0x5A5A5A5A}
 SIGNED = {1: np.uint8, 2: np.int16, 4: np.int32}
 
@@ -84,8 +87,20 @@ def test_gather_blocks(ext, seed):
     assert tags.cpu().tolist() == slots.tolist()
 
 
+@pytest.mark.parametrize("sort", [False, True])
 @pytest.mark.parametrize("seed", SEEDS)
-def test_scatter_rows(ext, seed):
+def test_scatter_rows(ext, seed, sort):
+    """As built (staged order at these sizes), and with the pairs sorted by slot first, as
+    scatter_rows runs from 2^18 slots and 8 GiB (its thresholds lowered to zero)."""
+    before = ext.scatter_rows_ordering(0, 0) if sort else None
+    try:
+        scatter_rows_case(ext, seed)
+    finally:
+        if before is not None:
+            ext.scatter_rows_ordering(*before)
+
+
+def scatter_rows_case(ext, seed):
     c = random_case(seed)
     cpu, base_cpu, gpu, base_gpu = on_device(c)
     e = cpu[0].element_size()
