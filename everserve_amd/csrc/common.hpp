@@ -88,15 +88,14 @@ inline bool aligned16(int64_t v) { return (v & 15) == 0; }
 // bytes ran at 35-56 GB/s; host-to-device pitched copies kept 56 GB/s, and splitting them into
 // one copy a run cost a restore 5-20 % in submission gaps.
 constexpr int64_t kMinRunCopyBytes = int64_t{1} << 20;
-// Which engine moves a copy, as this ROCm runs them on MI355X (kernel traces): hipMemcpyAsync
-// between HBM and pinned host memory, 32 KiB to 32 MiB either way, runs as a blit kernel on a
-// compute queue (8 MiB device-to-host: 151 us of kernel, 42-47 GB/s); hipMemcpy2DAsync, pitched
-// or not, even one row, runs on a DMA engine and launches no kernel (8 MiB: 161 us, 52 GB/s).
+// Which engine moves a copy depends on whether a profiler is attached. Under rocprofv3's kernel
+// trace, hipMemcpyAsync between HBM and pinned host memory (32 KiB to 32 MiB, either way) shows
+// as a blit kernel on a compute queue and hipMemcpy2DAsync as a DMA-engine copy; without the
+// profiler the contiguous device-to-host copy of 640 MiB ran at 56.9 GB/s, the DMA engines'
+// rate, against 54.6 GB/s under the trace and with the DMA engines turned off (blit kernels).
 // Sending every host copy through hipMemcpy2DAsync was measured against the forms below on a
-// Llama-3-8B decode step that stages 8 MiB a step: the snapshot added 40-47 us a step either way
-// (10 interleaved rounds of 100 steps). The forms below stay: their contiguous copies and
-// device-to-host runs of 1 MiB or more go as blit kernels, which the background clearing above
-// does not slow.
+// Llama-3-8B decode step that stages 8 MiB a step, without the profiler: the snapshot added
+// 40-47 us a step either way (10 interleaved rounds of 100 steps).
 
 inline int copy_runs(void* dst, int64_t dpitch, const void* src, int64_t spitch, int64_t len,
                      int64_t runs, hipMemcpyKind kind, hipStream_t stream) {
