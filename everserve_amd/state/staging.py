@@ -347,6 +347,14 @@ class StepStager:
         ``bytes_staged`` counts every row copied to the host, padding included; ``bytes_sent``
         only the rows of real slots, as the reference's record does (mirror.py:785-787)."""
         self._copy_stream = torch.cuda.Stream(device=self.device)
+        # The first pitched copy to the host in a process sets up the copy engine's queue, about
+        # 6 ms on MI355X: one of a few bytes here keeps that out of the first step's delivery.
+        probe = torch.empty(64, dtype=torch.uint8, device=self.device)  # its bytes are not read
+        with torch.cuda.stream(self._copy_stream):
+            ext.copy_rows_async(self._bounce[0].data_ptr(), probe.data_ptr(), 2, 16, 32,
+                                self.device)
+        self._copy_stream.synchronize()
+        del probe
         self._ready = ext.event_create(True)  # the host reads what this one orders
         self._queue: queue.Queue[StagedJob | None] = queue.Queue()
         self._thread = threading.Thread(target=self._copy_loop, daemon=True,
