@@ -696,17 +696,16 @@ def bench_c4(ext, steps, warmup):
     torch.cuda.synchronize()
     ok = bool(torch.equal(back.view(torch.int16), rows[:4].view(torch.int16)))
 
-    # the same call with its sorting turned off: the writes in staged order
-    before = ext.scatter_rows_ordering(-1, -1)
-    try:
-        for t in caches[:4]:
-            t.zero_()
-        per_s, _ = time_launches(scatter, steps, warmup, stream)
-        ext.gather_rows(ptrs[:4], s, heads, back.data_ptr(), n, D, BS, strides, 2)
-        torch.cuda.synchronize()
-        ok_s = bool(torch.equal(back.view(torch.int16), rows[:4].view(torch.int16)))
-    finally:
-        ext.scatter_rows_ordering(*before)
+    # the same call in staged order (evs_scatter_rows alone)
+    def staged():
+        ext.scatter_rows(ptrs, s, heads, rows.data_ptr(), n, D, BS, strides, 2, ordered=False)
+
+    for t in caches[:4]:
+        t.zero_()
+    per_s, _ = time_launches(staged, steps, warmup, stream)
+    ext.gather_rows(ptrs[:4], s, heads, back.data_ptr(), n, D, BS, strides, 2)
+    torch.cuda.synchronize()
+    ok_s = bool(torch.equal(back.view(torch.int16), rows[:4].view(torch.int16)))
 
     # the same restore with its writes in cache order: the (slot, staged row) pairs sorted by slot
     # on the host from the block table, then scatter_pairs
@@ -769,18 +768,19 @@ def bench_c4(ext, steps, warmup):
     return {
         "config": "C4 restore: [32,8,262144,2,128] bf16 rows into a fresh 16384-block cache, "
                   "random-permutation block table (64 seqs x 4096 tokens)",
-        "paths": "scatter_* here: evs_scatter_rows as built, which at this size sorts its "
-                 "(slot, row) pairs by slot on the device and writes them through the pair "
-                 "scatter (the sort inside each timed call); staged_order: the same call with "
-                 "the sorting off; the Restorer (a restore from the store's tables) launches "
-                 "evs_scatter_ranges, measured in by_ranges_in_slot_order",
+        "paths": "scatter_* here: the loader's scatter_rows as it chooses, which at this size "
+                 "sorts the (slot, row) pairs by slot on the device (evs_order_pairs) and writes "
+                 "them through the pair scatter (evs_scatter_pairs), the sort inside each timed "
+                 "call; staged_order: scatter_rows(ordered=False), evs_scatter_rows alone; the "
+                 "Restorer (a restore from the store's tables) launches evs_scatter_ranges, "
+                 "measured in by_ranges_in_slot_order",
         "scatter_ms": round(ms, 3),
         "scatter_gbs": round(2 * payload / ms / 1e6, 1),
         "scatter_frac_of_8tbs": round(2 * payload / ms / 1e6 / PEAK_HBM_GBS, 4),
         "round_trip_equal_first_4_layers": ok,
         "staged_order": {
-            "how": "evs_scatter_rows with evs_scatter_rows_ordering(-1, -1): one kernel, the "
-                   "rows read in staged order, each half-row written at its slot",
+            "how": "scatter_rows(ordered=False): evs_scatter_rows, one kernel, the rows read "
+                   "in staged order, each half-row written at its slot",
             "scatter_ms": round(ms_s, 3),
             "scatter_gbs": round(2 * payload / ms_s / 1e6, 1),
             "scatter_frac_of_8tbs": round(2 * payload / ms_s / 1e6 / PEAK_HBM_GBS, 4),
@@ -1703,8 +1703,8 @@ def pmc_workload(ext, which="gather", launches=5):
     read against.
 
     gather: the C2 gather. scatter: the C4 restore scatter (32 layers, 64 GiB moved) through
-    scatter_rows as built (at this size: its pairs sorted on the device, then the pair scatter).
-    staged: the same call with the sorting off (one kernel, staged order). pairs: the same restore
+    the loader's scatter_rows as it chooses (at this size: its pairs sorted on the device, then
+    the pair scatter). staged: scatter_rows(ordered=False), one kernel in staged order. pairs: the same restore
     in cache order (scatter_pairs, the pairs sorted by slot on the host). ranges: the same rows
     restored as one written range per layer, slots 0..n-1 in order (scatter_ranges, as the
     Restorer launches it, at C4's size). reduce: the C5 local
@@ -1749,7 +1749,6 @@ def pmc_workload(ext, which="gather", launches=5):
             os_dev, or_dev = torch.from_numpy(o_slots).to(dev), torch.from_numpy(o_rows).to(dev)
         starts = torch.zeros(1, dtype=torch.long, device=dev)
         first_rows = torch.tensor([0, n], dtype=torch.long, device=dev)
-        before = ext.scatter_rows_ordering(-1, -1) if which == "staged" else None
         for _ in range(launches):
             if which == "ranges":
                 ext.scatter_ranges(ptrs, starts, first_rows, n, heads, rows.data_ptr(), n, D, BS,
@@ -1758,9 +1757,8 @@ def pmc_workload(ext, which="gather", launches=5):
                 ext.scatter_pairs(ptrs, os_dev, or_dev, heads, rows.data_ptr(), n, D, BS, strides,
                                   2)
             else:
-                ext.scatter_rows(ptrs, s, heads, rows.data_ptr(), n, D, BS, strides, 2)
-        if before is not None:
-            ext.scatter_rows_ordering(*before)
+                ext.scatter_rows(ptrs, s, heads, rows.data_ptr(), n, D, BS, strides, 2,
+                                 ordered=which != "staged")
         algo = 2 * L * H * n * 2 * D * 2
         del rows, caches
     elif which == "reduce":

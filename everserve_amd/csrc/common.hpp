@@ -6,7 +6,6 @@
 
 #include <cstdint>
 #include <cstdio>
-#include <functional>
 #include <string>
 
 #include "everserve_mi355x.h"
@@ -114,15 +113,5 @@ inline int copy_runs(void* dst, int64_t dpitch, const void* src, int64_t spitch,
   }
   return EVS_OK;
 }
-
-// Runs `scatter` on the pairs (slots[t], t), t < n, sorted by slot on stream s (order.hip): the
-// sort and the scatter's reads of the sorted pairs use a workspace the library keeps per device,
-// allocated on the first such call and grown when a call needs more. Calls on one device take
-// turns with the workspace: each waits, on its own stream, for the previous one's scatter. When
-// the stream is being captured into a graph (the sort clears its counters with hipMemsetAsync) or
-// no workspace can be had, *ordered is false and nothing is enqueued.
-using PairScatter = std::function<int(const int64_t* slots, const int64_t* rows_of)>;
-int with_slot_order(const int64_t* slots, int64_t n, hipStream_t s, const PairScatter& scatter,
-                    bool* ordered);
 
 }  // namespace evs

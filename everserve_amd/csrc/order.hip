@@ -68,66 +68,7 @@ int scratch_here(void** out) {
   return EVS_OK;
 }
 
-// evs_scatter_rows's workspace on one device: [sorted slots | their rows | row numbers and
-// rocPRIM's storage], and an event recorded after the last call's scatter.
-struct OrderSpace {
-  std::mutex lock;
-  char* ptr = nullptr;
-  int64_t bytes = 0;
-  hipEvent_t used = nullptr;
-};
-OrderSpace g_order_space[kMaxDevices];
-constexpr int kOrderKeyBits = 32;  // slot ids past 2^32 sort by their low bits: the order is then
-                                   // only partial, and every write still lands at its own slot
-
 }  // namespace
-
-int with_slot_order(const int64_t* slots, int64_t n, hipStream_t s, const PairScatter& scatter,
-                    bool* ordered) {
-  *ordered = false;
-  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
-  EVS_HIP(hipStreamIsCapturing(s, &capture));
-  if (capture != hipStreamCaptureStatusNone) return EVS_OK;
-  int dev = -1;
-  EVS_HIP(hipGetDevice(&dev));
-  if (dev < 0 || dev >= kMaxDevices) return EVS_OK;
-  int64_t order_bytes = 0;  // evs_order_pairs's workspace: row numbers and rocPRIM's storage
-  int rc = evs_order_pairs_workspace(n, kOrderKeyBits, &order_bytes);
-  if (rc != EVS_OK) return rc;
-  const int64_t half = round_up(n * 8);
-  const int64_t need = 2 * half + order_bytes;
-
-  OrderSpace& w = g_order_space[dev];
-  std::lock_guard<std::mutex> hold(w.lock);
-  if (w.used == nullptr) EVS_HIP(hipEventCreateWithFlags(&w.used, hipEventDisableTiming));
-  if (w.bytes < need) {
-    if (w.ptr != nullptr) {
-      EVS_HIP(hipEventSynchronize(w.used));
-      EVS_HIP(hipFree(w.ptr));
-      w.ptr = nullptr;
-      w.bytes = 0;
-    }
-    const int64_t grown = round_up(need + need / 4);
-    void* p = nullptr;
-    if (hipMalloc(&p, static_cast<size_t>(grown)) != hipSuccess) {
-      (void)hipGetLastError();  // no room: the caller writes in staged order instead
-      return EVS_OK;
-    }
-    w.ptr = static_cast<char*>(p);
-    w.bytes = grown;
-  }
-  EVS_HIP(hipStreamWaitEvent(s, w.used, 0));
-  *ordered = true;
-  int64_t* sorted_slots = reinterpret_cast<int64_t*>(w.ptr);
-  int64_t* rows_of = reinterpret_cast<int64_t*>(w.ptr + half);
-  rc = evs_order_pairs(slots, n, kOrderKeyBits, sorted_slots, rows_of, w.ptr + 2 * half,
-                       w.bytes - 2 * half, s);
-  if (rc == EVS_OK) rc = scatter(sorted_slots, rows_of);
-  const hipError_t recorded = hipEventRecord(w.used, s);
-  if (rc == EVS_OK) EVS_HIP(recorded);
-  return rc;
-}
-
 }  // namespace evs
 
 extern "C" int evs_order_pairs_workspace(int64_t num_pairs, int key_bits, int64_t* bytes) {

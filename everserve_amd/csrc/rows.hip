@@ -28,8 +28,6 @@
 // its latency; each wave reading its own rows' ids with scalar loads, no LDS and no barrier
 // (2 % slower: the per-lane choice among the wave's rows costs more than the barrier).
 
-#include <atomic>
-
 #include "common.hpp"
 
 namespace evs {
@@ -550,11 +548,8 @@ struct RowsCall {
   int64_t nranges = 0;                  // kByRanges
 };
 
-// Plans the launch and, unless `dry`, enqueues it; a dry run makes every check and enqueues
-// nothing.
 template <int D, int I, typename T>
-int launch_typed(RowsArgs a, int64_t L, uint32_t W, hipStream_t stream, const char* name,
-                 bool dry) {
+int launch_typed(RowsArgs a, int64_t L, uint32_t W, hipStream_t stream, const char* name) {
   const int64_t target = I == kByPairs ? EVS_PAIRS_TILE_WORDS
                          : D == kGather ? EVS_GATHER_TILE_WORDS : EVS_SCATTER_TILE_WORDS;
   const int hpt = I == kByPairs ? EVS_PAIRS_HEADS_PER_TILE
@@ -586,7 +581,6 @@ int launch_typed(RowsArgs a, int64_t L, uint32_t W, hipStream_t stream, const ch
   a.div_ts = FastDiv(static_cast<uint32_t>(ts));
   a.div_tiles = FastDiv(static_cast<uint32_t>(tiles));
   a.div_groups = FastDiv(static_cast<uint32_t>(groups));
-  if (dry) return EVS_OK;
   hipLaunchKernelGGL((move_rows<T, D, I>), dim3(static_cast<uint32_t>(grid)),
                      dim3(threads_of(D, I)), 0, stream, a);
   EVS_LAUNCHED(name);
@@ -624,20 +618,8 @@ int check_call(const RowsCall& c, const char* name, bool* moves) {
   return EVS_OK;
 }
 
-// evs_scatter_rows writes in slot order (sorting its pairs first, through the pair scatter) when
-// a call moves at least this many rows and bytes; a negative value turns that off. In staged
-// order each 256-byte half-row store lands at a random place; in slot order the writes run
-// through each layer's cache front to back. Measured on MI355X (Llama-3-8B rows, bf16, 16-slot
-// blocks of a permuted table, median of 10 launches): every slot of a 262,144-slot cache, 32
-// layers: 11.58 against 12.17 ms (sort 0.11 ms included); 8 layers 2.86 against 3.02 ms; 4 layers
-// 1.52 against 1.53; 1 layer 0.47 against 0.38 (the sort not repaid); a quarter of the cache's
-// blocks, 32 layers: 3.12 against 3.08 ms (writes spread over a sparse subset gain nothing from
-// order).
-std::atomic<int64_t> g_order_min_rows{int64_t{1} << 18};
-std::atomic<int64_t> g_order_min_bytes{int64_t{8} << 30};
-
 template <int D, int I>
-int move(const RowsCall& c, const char* name, bool dry = false) {
+int move(const RowsCall& c, const char* name) {
   bool moves = false;
   const int rc = check_call<D, I>(c, name, &moves);
   if (rc != EVS_OK || !moves) return rc;
@@ -675,33 +657,18 @@ int move(const RowsCall& c, const char* name, bool dry = false) {
                        aligned16(a.so) && aligned16(a.sh) && aligned16(a.skv);
   if (vectors) {
     a.sj = 16;
-    return launch_typed<D, I, u32x4>(a, c.L, static_cast<uint32_t>(c.d * e / 16), c.stream, name,
-                                     dry);
+    return launch_typed<D, I, u32x4>(a, c.L, static_cast<uint32_t>(c.d * e / 16), c.stream, name);
   }
   a.sj = c.strides[4] * e;
   EVS_REQUIRE(c.d < (int64_t{1} << 24), "%s: head_dim too large", name);
   switch (e) {
     case 1:
-      return launch_typed<D, I, uint8_t>(a, c.L, static_cast<uint32_t>(c.d), c.stream, name, dry);
+      return launch_typed<D, I, uint8_t>(a, c.L, static_cast<uint32_t>(c.d), c.stream, name);
     case 2:
-      return launch_typed<D, I, uint16_t>(a, c.L, static_cast<uint32_t>(c.d), c.stream, name,
-                                          dry);
+      return launch_typed<D, I, uint16_t>(a, c.L, static_cast<uint32_t>(c.d), c.stream, name);
     default:
-      return launch_typed<D, I, uint32_t>(a, c.L, static_cast<uint32_t>(c.d), c.stream, name,
-                                          dry);
+      return launch_typed<D, I, uint32_t>(a, c.L, static_cast<uint32_t>(c.d), c.stream, name);
   }
-}
-
-// Whether evs_scatter_rows sorts the call's pairs first (the thresholds above). The sort takes at
-// most 2^31 - 1 pairs.
-bool worth_ordering(const RowsCall& c) {
-  const int64_t min_rows = g_order_min_rows.load(), min_bytes = g_order_min_bytes.load();
-  if (min_rows < 0 || min_bytes < 0) return false;
-  if (c.n_index < min_rows || c.n_index >= (int64_t{1} << 31)) return false;
-  const double bytes = static_cast<double>(c.L) * static_cast<double>(c.H) *
-                       static_cast<double>(c.n_index) * 2.0 * static_cast<double>(c.d) *
-                       static_cast<double>(c.elem);
-  return bytes >= static_cast<double>(min_bytes);
 }
 
 }  // namespace
@@ -741,41 +708,7 @@ extern "C" int evs_scatter_rows(const int64_t* layer_ptrs, int64_t num_layers,
   evs::RowsCall c{layer_ptrs, num_layers, slots, nullptr, num_slots, heads, num_heads,
                   const_cast<char*>(static_cast<const char*>(in)), capacity, head_dim,
                   block_size, strides, elem_size, nullptr, nullptr, evs::as_stream(stream)};
-  bool moves = false;
-  int rc = evs::check_call<evs::kScatter, evs::kBySlots>(c, "evs_scatter_rows", &moves);
-  if (rc != EVS_OK || !moves) return rc;
-  if (evs::worth_ordering(c)) {
-    // the same writes in slot order, through the pair scatter: (slots[t], t) sorted by slot.
-    // Its launch is checked first, so that a refusal leaves nothing enqueued.
-    evs::RowsCall plan = c;
-    plan.rows_of = slots;
-    rc = evs::move<evs::kScatter, evs::kByPairs>(plan, "evs_scatter_rows", /*dry=*/true);
-    if (rc != EVS_OK) return rc;
-    bool ordered = false;
-    rc = evs::with_slot_order(
-        slots, num_slots, c.stream,
-        [&c](const int64_t* sorted_slots, const int64_t* rows_of) {
-          evs::RowsCall p = c;
-          p.slots = sorted_slots;
-          p.rows_of = rows_of;
-          return evs::move<evs::kScatter, evs::kByPairs>(p, "evs_scatter_rows");
-        },
-        &ordered);
-    if (ordered || rc != EVS_OK) return rc;
-  }
   return evs::move<evs::kScatter, evs::kBySlots>(c, "evs_scatter_rows");
-}
-
-extern "C" int evs_scatter_rows_ordering(int64_t min_rows, int64_t min_bytes,
-                                         int64_t* previous) {
-  evs::clear_error();
-  if (previous != nullptr) {
-    previous[0] = evs::g_order_min_rows.load();
-    previous[1] = evs::g_order_min_bytes.load();
-  }
-  evs::g_order_min_rows.store(min_rows);
-  evs::g_order_min_bytes.store(min_bytes);
-  return EVS_OK;
 }
 
 extern "C" int evs_scatter_pairs(const int64_t* layer_ptrs, int64_t num_layers,

@@ -48,6 +48,16 @@ _PACKAGE = Path(__file__).resolve().parent
 EVS_OK = 0
 REDUCE_STATE_WORDS = 288
 """64-bit words of local_reduce's state record (EVS_REDUCE_STATE_WORDS in the C header)."""
+ORDER_MIN_SLOTS = 1 << 18
+ORDER_MIN_BYTES = 8 << 30
+"""The sizes from which :meth:`Kernels.scatter_rows` sorts its pairs by slot first. Measured on
+MI355X (Llama-3-8B rows, bf16, 16-slot blocks of a permuted table, median of 10 launches), sorted
+against staged order, the sort's 0.11 ms included: every slot of a 262,144-slot cache, 32 layers,
+11.58 against 12.17 ms; 8 layers 2.86 against 3.02; 4 layers 1.52 against 1.53; 1 layer 0.47
+against 0.38 (the sort not repaid); a quarter of the cache's blocks, 32 layers, 3.12 against 3.08
+(writes spread over a sparse part of a cache gain nothing from order). The call cannot see the
+cache's size, so a call of this many slots into a cache several times larger sorts too, and can
+lose up to about 3 %: pass ``ordered=False`` there."""
 
 
 class BoundGather:
@@ -186,7 +196,6 @@ _SIGNATURES: tuple[tuple[str, object, tuple], ...] = (
         (_P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _P, _I64, _P, _P),
     ),
     ("evs_scatter_rows", _I32, (_P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _P, _I64, _P)),
-    ("evs_scatter_rows_ordering", _I32, (_I64, _I64, _P)),
     ("evs_scatter_pairs", _I32,
      (_P, _I64, _P, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _P, _I64, _P)),
     ("evs_scatter_ranges", _I32,
@@ -280,6 +289,7 @@ class Kernels:
         self._check(lib.evs_layout_constants(words, 5))
         self.MAX_ROWS, self.CTRL_WORDS, self.ABORT, self.LATE, self.BOUND = (int(w) for w in words)
         self._workspace: dict = {}  # order_pairs' workspace, per (device, stream)
+        self._pairs: dict = {}  # scatter_rows' sorted pairs, per (device, stream)
 
     def _check(self, rc: int) -> None:
         if rc != EVS_OK:
@@ -390,11 +400,20 @@ class Kernels:
         block_size: int,
         strides: Sequence[int],
         elem_size: int,
+        ordered: bool | None = None,
     ) -> None:
         """Write [L, H, cap, 2, d] rows back into the caches at ``slots`` and head slots ``heads``.
 
         The inverse of :meth:`gather_rows`; negative slots are padding and are skipped. Replaces
         the restore's ``PagedKV.write_rows`` (core/everserve/state/kvcopy.py:118-128).
+
+        ``ordered``: write in slot order, the (slot, row) pairs sorted on the device first
+        (:meth:`order_pairs`, then :meth:`scatter_pairs`, in the workspace this object keeps per
+        device and stream), or in staged order (``evs_scatter_rows``, one kernel). The same bytes
+        land either way. ``None`` sorts from :data:`ORDER_MIN_SLOTS` slots and
+        :data:`ORDER_MIN_BYTES` of rows, where writing a whole cache through a permuted block
+        table in slot order repays the sort, and never under graph capture (the sort clears its
+        counters with a memset, which a captured graph must not hold).
         """
         import torch
 
@@ -405,22 +424,40 @@ class Kernels:
         hp = _device_ptr(heads, "scatter_rows: heads", torch.long)
         _one_device("scatter_rows", layer_ptrs, slots, heads)
         st = (ctypes.c_int64 * 5)(*[int(s) for s in strides])
+        n, nl, nh = slots.numel(), layer_ptrs.numel(), heads.numel()
         with torch.cuda.device(slots.device):
-            self._check(
-                self._lib.evs_scatter_rows(
-                    lp, layer_ptrs.numel(), sp, slots.numel(), hp, heads.numel(), int(in_ptr),
-                    int(capacity), int(d), int(block_size), st, int(elem_size),
-                    _stream_of(slots.device),
+            capturing = torch.cuda.is_current_stream_capturing()
+            if ordered is None:
+                ordered = (not capturing and ORDER_MIN_SLOTS <= n < (1 << 31)
+                           and nl * nh * n * 2 * int(d) * int(elem_size) >= ORDER_MIN_BYTES)
+            if ordered and capturing:
+                raise RuntimeError("scatter_rows: an ordered scatter cannot be captured in a graph "
+                                   "(its sort clears counters with a memset)")
+            if not ordered:
+                self._check(
+                    self._lib.evs_scatter_rows(
+                        lp, nl, sp, n, hp, nh, int(in_ptr), int(capacity), int(d),
+                        int(block_size), st, int(elem_size), _stream_of(slots.device),
+                    )
                 )
+                return
+            # the staged-order call's checks first (no layer: nothing is launched), so that the
+            # ordered call refuses what the staged one refuses
+            self._check(
+                self._lib.evs_scatter_rows(lp, 0, sp, n, hp, nh, int(in_ptr), int(capacity),
+                                           int(d), int(block_size), st, int(elem_size),
+                                           _stream_of(slots.device))
             )
-
-    def scatter_rows_ordering(self, min_rows: int, min_bytes: int) -> tuple[int, int]:
-        """Set the sizes from which :meth:`scatter_rows` sorts its pairs by slot before writing
-        (at least ``min_rows`` slots and ``min_bytes`` of rows; negative: never); returns the
-        values in force before. Process-wide."""
-        prev = (ctypes.c_int64 * 2)()
-        self._check(self._lib.evs_scatter_rows_ordering(int(min_rows), int(min_bytes), prev))
-        return int(prev[0]), int(prev[1])
+            if n == 0 or nl == 0 or nh == 0:
+                return
+            key = (slots.device, _stream_of(slots.device))
+            pairs = self._pairs.get(key)
+            if pairs is None or pairs[0].numel() < n:
+                pairs = self._pairs[key] = (torch.empty(n, dtype=torch.long, device=slots.device),
+                                            torch.empty(n, dtype=torch.long, device=slots.device))
+            o_slots, o_rows = self.order_pairs(slots, 1 << 32, out=(pairs[0][:n], pairs[1][:n]))
+        self.scatter_pairs(layer_ptrs, o_slots, o_rows, heads, in_ptr, capacity, d, block_size,
+                           strides, elem_size)
 
     def scatter_pairs(
         self,

@@ -96,27 +96,15 @@ int evs_gather_blocks(const int64_t* layer_ptrs, int64_t num_layers, const int32
  * head_dim] back into the paged caches at slots[t] and head slots heads[h]. A negative slot is
  * padding and is skipped (nothing written). Slots must be distinct (a restore's written slot
  * ranges are, store/src/storage.rs:430-451); with duplicates which row lands is unspecified.
- * A call of at least 2^18 slots and 8 GiB of rows (see evs_scatter_rows_ordering) sorts its
- * (slot, row) pairs by slot on the stream first and writes in that order through the pair scatter:
- * the first such call on a device allocates a workspace of about 24 bytes a slot that the library
- * keeps (and grows) for later ones; calls on one device take turns with it, each waiting on its
- * own stream for the previous one. A call on a stream under graph capture, or one for which no
- * workspace can be had, writes in staged order. The first such call allocates with hipMalloc,
- * which a graph capture in global mode elsewhere in the process forbids: make it before such a
- * capture starts, or turn the sorting off. Replaces the restore's per-table
- * PagedKV.write_rows scatter (core/everserve/state/mirror.py:926-937,
- * core/everserve/state/kvcopy.py:118-128). */
+ * One kernel, rows read in staged order, nothing allocated. For a restore that writes a whole
+ * cache through a permuted block table, evs_order_pairs then evs_scatter_pairs write the same
+ * bytes in slot order, faster (the shipped loader's scatter_rows does so from 2^18 slots and
+ * 8 GiB of rows, in a workspace it keeps). Replaces the restore's per-table PagedKV.write_rows
+ * scatter (core/everserve/state/mirror.py:926-937, core/everserve/state/kvcopy.py:118-128). */
 int evs_scatter_rows(const int64_t* layer_ptrs, int64_t num_layers, const int64_t* slots,
                      int64_t num_slots, const int64_t* heads, int64_t num_heads, const void* in,
                      int64_t capacity, int64_t head_dim, int64_t block_size,
                      const int64_t* strides, int64_t elem_size, void* stream);
-
-/* The sizes from which evs_scatter_rows sorts its pairs first: at least min_rows slots and
- * min_bytes of rows (num_layers * num_heads * num_slots * 2 * head_dim * elem_size); a negative
- * value turns the sorting off. The defaults are 2^18 and 8 GiB. When previous is not NULL it
- * receives the two values in force before the call. Process-wide, for every device. No
- * counterpart in the reference: a tuning knob of this library's write order. */
-int evs_scatter_rows_ordering(int64_t min_rows, int64_t min_bytes, int64_t* previous);
 
 /* The scatter by (slot, staged row) pairs: for every listed i, layer and head index h, write staged
  * row rows_of[i] of [num_layers, num_heads, capacity, 2, head_dim] into the cache at slot slots[i]

@@ -117,23 +117,6 @@ def test_a_launch_past_the_work_item_limit_is_refused_before_launch(lib):
     rc = lib.evs_scatter_ranges(fake, 32, fake, fake, 1, 2 * n, fake, 8, ctypes.c_void_p(1 << 21),
                                 2 * n, 128, 16, strides, 2, None)
     assert rc == 1 and b"work-items" in lib.evs_last_error()
-    # the same scatter_rows call in staged order (sorting off) is refused the same way
-    prev = (ctypes.c_int64 * 2)()
-    assert lib.evs_scatter_rows_ordering(-1, -1, prev) == 0
-    try:
-        rc = lib.evs_scatter_rows(fake, 32, fake, 2 * n, fake, 8, ctypes.c_void_p(1 << 21), 2 * n,
-                                  128, 16, strides, 2, None)
-        assert rc == 1 and b"work-items" in lib.evs_last_error()
-    finally:
-        lib.evs_scatter_rows_ordering(prev[0], prev[1], None)
-
-
-def test_scatter_rows_sorts_from_two_to_the_18_slots_and_8_gib_by_default(lib):
-    prev = (ctypes.c_int64 * 2)()
-    assert lib.evs_scatter_rows_ordering(5, 6, prev) == 0
-    assert list(prev) == [1 << 18, 8 << 30]
-    assert lib.evs_scatter_rows_ordering(prev[0], prev[1], prev) == 0
-    assert list(prev) == [5, 6]
 
 
 def test_failed_parity_flags_fail_the_bench(tmp_path):

@@ -44,26 +44,17 @@ def test_the_gather_writes_the_stored_rows(ext, case):
     assert np.array_equal(out.cpu().numpy().view(want.dtype).reshape(want.shape), want)
 
 
-@pytest.mark.parametrize("sort", [False, True])
+@pytest.mark.parametrize("ordered", [None, True])
 @pytest.mark.parametrize("case", [c for c in CASES if c.endswith("bf16")])
-def test_the_scatter_writes_the_stored_caches(ext, case, sort):
+def test_the_scatter_writes_the_stored_caches(ext, case, ordered):
     """scatter_rows as it runs at these sizes (staged order), and with its pairs sorted by slot
-    first, as it runs from 2^18 slots and 8 GiB (the thresholds lowered to zero)."""
-    before = ext.scatter_rows_ordering(0, 0) if sort else None
-    try:
-        scatter_and_check(ext, case)
-    finally:
-        if before is not None:
-            ext.scatter_rows_ordering(*before)
-
-
-def scatter_and_check(ext, case):
+    first, as it runs from 2^18 slots and 8 GiB."""
     layers = [torch.zeros_like(t).cuda() for t in tensors(case)]
     rows = torch.from_numpy(G[f"{case}_rows"].view(np.int16).copy()).cuda()
     d = int(case.rsplit("_", 2)[1][1:])
     ext.scatter_rows(dev_long([t.data_ptr() for t in layers]), dev_long(G["slots"]),
                      dev_long(G["heads"]), rows.data_ptr(), int(G["capacity"]), d,
-                     int(G["block_size"]), list(strides_of(layers[0])), 2)
+                     int(G["block_size"]), list(strides_of(layers[0])), 2, ordered=ordered)
     torch.cuda.synchronize()
     got = np.stack([mf.raw(t.cpu()) for t in layers])
     assert np.array_equal(got, G[f"{case}_scattered"])

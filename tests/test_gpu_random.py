@@ -87,20 +87,11 @@ def test_gather_blocks(ext, seed):
     assert tags.cpu().tolist() == slots.tolist()
 
 
-@pytest.mark.parametrize("sort", [False, True])
+@pytest.mark.parametrize("ordered", [None, True])
 @pytest.mark.parametrize("seed", SEEDS)
-def test_scatter_rows(ext, seed, sort):
-    """As built (staged order at these sizes), and with the pairs sorted by slot first, as
-    scatter_rows runs from 2^18 slots and 8 GiB (its thresholds lowered to zero)."""
-    before = ext.scatter_rows_ordering(0, 0) if sort else None
-    try:
-        scatter_rows_case(ext, seed)
-    finally:
-        if before is not None:
-            ext.scatter_rows_ordering(*before)
-
-
-def scatter_rows_case(ext, seed):
+def test_scatter_rows(ext, seed, ordered):
+    """As scatter_rows runs at these sizes (staged order), and with the pairs sorted by slot
+    first, as it runs from 2^18 slots and 8 GiB."""
     c = random_case(seed)
     cpu, base_cpu, gpu, base_gpu = on_device(c)
     e = cpu[0].element_size()
@@ -109,7 +100,7 @@ def scatter_rows_case(ext, seed):
                         strides_of(cpu[0]), e)
     rows = torch.from_numpy(staged.view(SIGNED[e])).cuda()
     ext.scatter_rows(ptrs(gpu), dev_long(c["slots"]), dev_long(c["heads"]), rows.data_ptr(),
-                     c["cap"], c["d"], c["bs"], list(strides_of(gpu[0])), e)
+                     c["cap"], c["d"], c["bs"], list(strides_of(gpu[0])), e, ordered=ordered)
     torch.cuda.synchronize()
     for a, b in zip(base_gpu, base_cpu):
         assert np.array_equal(bits(a), bits(b))

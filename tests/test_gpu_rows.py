@@ -75,29 +75,13 @@ def test_block_gather_equals_the_gather_of_the_expanded_slots(ext, layout, d):
     assert tags.cpu().tolist() == slots.tolist()
 
 
-@pytest.fixture
-def sorted_first(ext):
-    """scatter_rows sorting its pairs by slot at every size, for the test's length."""
-    before = ext.scatter_rows_ordering(0, 0)
-    yield
-    ext.scatter_rows_ordering(*before)
-
-
-@pytest.fixture
-def staged_only(ext):
-    """scatter_rows writing in staged order at every size, for the test's length."""
-    before = ext.scatter_rows_ordering(-1, -1)
-    yield
-    ext.scatter_rows_ordering(*before)
-
-
-@pytest.mark.parametrize("order", ["as built", "sorted first"])
+@pytest.mark.parametrize("ordered", [None, True])
 @pytest.mark.parametrize("layout", LAYOUTS)
 @pytest.mark.parametrize("d", [8, 6])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float8_e4m3fn])
-def test_scatter_writes_exactly_what_the_oracle_writes(ext, request, order, layout, d, dtype):
-    if order == "sorted first":
-        request.getfixturevalue("sorted_first")
+def test_scatter_writes_exactly_what_the_oracle_writes(ext, ordered, layout, d, dtype):
+    """As scatter_rows runs at this size (staged order), and with its pairs sorted by slot first
+    (order_pairs, then scatter_pairs), as it runs from 2^18 slots and 8 GiB."""
     src = caches(layout, d, dtype, seed=5)
     dst = caches(layout, d, dtype, seed=9)  # a cache that already holds other rows
     _, _, bs, _ = oracle.recognise(src[0].shape)
@@ -109,7 +93,7 @@ def test_scatter_writes_exactly_what_the_oracle_writes(ext, request, order, layo
     rows = torch.from_numpy(staged.copy()).cuda()
     ext.scatter_rows(ptrs(gpu_dst), torch.tensor(SLOTS, dtype=torch.long, device="cuda"),
                      torch.tensor(target, dtype=torch.long, device="cuda"), rows.data_ptr(),
-                     CAPACITY, d, bs, list(strides_of(gpu_dst[0])), e)
+                     CAPACITY, d, bs, list(strides_of(gpu_dst[0])), e, ordered=ordered)
     torch.cuda.synchronize()
     for got, want in zip(gpu_dst, dst):
         assert np.array_equal(bits(got), bits(want))
@@ -133,6 +117,12 @@ def test_rejections_raise_not_launch(ext):
         ext.gather_rows(ptrs(layers), s.cpu(), h, out.data_ptr(), 8, 8, 4, st, 2)
     # nothing to move: returns without launching
     ext.gather_rows(ptrs(layers), s[:0], h, out.data_ptr(), 8, 8, 4, st, 2)
+    # the ordered scatter refuses what the staged one does, before it sorts anything
+    for ordered in (False, True):
+        with pytest.raises(KernelError, match="capacity"):
+            ext.scatter_rows(ptrs(layers), s, h, out.data_ptr(), 2, 8, 4, st, 2, ordered=ordered)
+        with pytest.raises(KernelError, match="element size"):
+            ext.scatter_rows(ptrs(layers), s, h, out.data_ptr(), 8, 8, 4, st, 3, ordered=ordered)
 
 
 def test_a_captured_gather_replays_like_an_eager_call(ext):
@@ -162,11 +152,11 @@ def test_a_captured_gather_replays_like_an_eager_call(ext):
         assert np.array_equal(bits(out), want), i
 
 
-def test_a_captured_scatter_writes_in_staged_order_and_replays_right(ext, sorted_first):
+def test_a_captured_scatter_writes_in_staged_order_and_replays_right(ext):
     """Under graph capture scatter_rows does not sort (the sort clears its counters with a memset,
-    which a captured graph must not hold), whatever its thresholds: the graph holds the staged
-    order's one kernel, and each replay writes what the oracle writes, the slot ids changed in
-    place between replays and the cache reset by eager work."""
+    which a captured graph must not hold), and asked to sort it refuses: the graph holds the
+    staged order's one kernel, and each replay writes what the oracle writes, the slot ids changed
+    in place between replays and the cache reset by eager work."""
     src = caches("kv_first", 8, torch.bfloat16, seed=5)
     base = caches("kv_first", 8, torch.bfloat16, seed=9)
     staged = oracle.gather_rows(src, SLOTS, HEADS, CAPACITY, 8, 4, strides_of(src[0]), 2)
@@ -180,6 +170,9 @@ def test_a_captured_scatter_writes_in_staged_order_and_replays_right(ext, sorted
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=side):
         ext.scatter_rows(table, s, h, rows.data_ptr(), CAPACITY, 8, 4, strides, 2)
+        with pytest.raises(RuntimeError, match="captured"):
+            ext.scatter_rows(table, s, h, rows.data_ptr(), CAPACITY, 8, 4, strides, 2,
+                             ordered=True)
     for i, slots in enumerate([SLOTS, [27, 3, -1, 9, 0], SLOTS[::-1]]):
         s.copy_(torch.tensor(slots))
         for g, b in zip(gpu, base):
@@ -193,11 +186,10 @@ def test_a_captured_scatter_writes_in_staged_order_and_replays_right(ext, sorted
             assert np.array_equal(bits(got), bits(w)), i
 
 
-def test_sorted_calls_on_two_streams_take_turns_with_the_workspace(ext, sorted_first):
+def test_sorted_calls_on_two_streams_keep_their_own_pairs(ext):
     """Two sorting scatters enqueued back to back on two streams, with no synchronisation between
-    them, share the library's workspace: the second waits for the first's scatter before its sort
-    writes the workspace again. Each cache ends as the oracle writes it; the second call's slots
-    are twice as many, so the workspace also grows between two calls in flight."""
+    them: each stream's sort writes its own workspace and pairs, so neither reads the other's.
+    Each cache ends as the oracle writes it."""
     L, NB, BS, H, D = 4, 256, 16, 4, 64
     rng = np.random.default_rng(61)
     shape = (2, NB, BS, H, D)
@@ -221,7 +213,7 @@ def test_sorted_calls_on_two_streams_take_turns_with_the_workspace(ext, sorted_f
             table = ptrs(gpu)
             keep += [s, rows, h, table]
             ext.scatter_rows(table, s, h, rows.data_ptr(), len(slots), D, BS,
-                             list(strides_of(gpu[0])), 2)
+                             list(strides_of(gpu[0])), 2, ordered=True)
     torch.cuda.synchronize()
     for slots, staged, base, gpu in jobs:
         want = [t.clone() for t in base]
@@ -369,8 +361,8 @@ def test_copy_rows_moves_only_the_filled_rows(ext):
 def test_c4_restore_round_trip_full_size(ext):
     """C4: 64 seqs x 4096 tokens of Llama-3-8B rows (32 GiB) scattered into a fresh
     16384-block cache through a seeded random-permutation block table, gathered back: equal,
-    three ways: scatter_rows as built (at this size it sorts its pairs on the device first),
-    scatter_rows in staged order, and scatter_pairs with the pairs sorted on the host."""
+    three ways: scatter_rows as it chooses (at this size it sorts its pairs on the device
+    first), scatter_rows in staged order, and scatter_pairs with the pairs sorted on the host."""
     L, NB, BS, H, D = 32, 16384, 16, 8, 128
     n = NB * BS
     rows = torch.empty((L, H, n, 2, D), dtype=torch.bfloat16, device="cuda")
@@ -389,11 +381,8 @@ def test_c4_restore_round_trip_full_size(ext):
         if how == "as built":
             ext.scatter_rows(ptrs(cache), s, heads, rows.data_ptr(), n, D, BS, strides, 2)
         elif how == "staged order":
-            before = ext.scatter_rows_ordering(-1, -1)
-            try:
-                ext.scatter_rows(ptrs(cache), s, heads, rows.data_ptr(), n, D, BS, strides, 2)
-            finally:
-                ext.scatter_rows_ordering(*before)
+            ext.scatter_rows(ptrs(cache), s, heads, rows.data_ptr(), n, D, BS, strides, 2,
+                             ordered=False)
         else:
             ext.scatter_pairs(ptrs(cache), torch.from_numpy(sorted_slots).cuda(),
                               torch.from_numpy(rows_of).cuda(), heads, rows.data_ptr(), n, D, BS,
