@@ -60,6 +60,14 @@ cache's size, so a call of this many slots into a cache several times larger sor
 lose up to about 3 %: pass ``ordered=False`` there."""
 
 
+def sort_first(n: int, layers: int, heads: int, d: int, elem: int, capturing: bool) -> bool:
+    """Whether :meth:`Kernels.scatter_rows` left to choose sorts its ``n`` pairs by slot first:
+    from :data:`ORDER_MIN_SLOTS` slots and :data:`ORDER_MIN_BYTES` of rows, fewer than 2^31
+    pairs (the sort's limit), and not while the stream is being captured."""
+    return (not capturing and ORDER_MIN_SLOTS <= n < (1 << 31)
+            and layers * heads * n * 2 * d * elem >= ORDER_MIN_BYTES)
+
+
 class BoundGather:
     """``evs_gather_rows`` for fixed layers, heads and layout (:meth:`Kernels.bind_gather`)."""
 
@@ -428,8 +436,7 @@ class Kernels:
         with torch.cuda.device(slots.device):
             capturing = torch.cuda.is_current_stream_capturing()
             if ordered is None:
-                ordered = (not capturing and ORDER_MIN_SLOTS <= n < (1 << 31)
-                           and nl * nh * n * 2 * int(d) * int(elem_size) >= ORDER_MIN_BYTES)
+                ordered = sort_first(n, nl, nh, int(d), int(elem_size), capturing)
             if ordered and capturing:
                 raise RuntimeError("scatter_rows: an ordered scatter cannot be captured in a graph "
                                    "(its sort clears counters with a memset)")

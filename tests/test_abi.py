@@ -128,3 +128,15 @@ def test_failed_parity_flags_fail_the_bench(tmp_path):
                      "s": {"k": {"sum_exact": False}}, "spot_check": False, "rows_check": True}}
     assert bench.failed_checks(bad) == ["extra.c4.round_trip_equal_first_4_layers",
                                         "extra.s.k.sum_exact", "extra.spot_check"]
+
+def test_scatter_rows_sorts_first_from_two_to_the_18_slots_and_8_gib():
+    sf = kernels.sort_first
+    c4 = dict(layers=32, heads=8, d=128, elem=2)  # 32 GiB of rows at 262,144 slots
+    assert sf(1 << 18, capturing=False, **c4)
+    assert not sf((1 << 18) - 1, capturing=False, **c4)  # too few slots
+    assert not sf(1 << 18, capturing=True, **c4)  # the sort's memset stays out of graphs
+    assert not sf(1 << 31, capturing=False, **c4)  # past the sort's limit
+    # 8 layers of the cache (8 GiB) sort, 4 layers (4 GiB) do not
+    assert sf(1 << 18, layers=8, heads=8, d=128, elem=2, capturing=False)
+    assert not sf(1 << 18, layers=4, heads=8, d=128, elem=2, capturing=False)
+    assert kernels.ORDER_MIN_SLOTS == 1 << 18 and kernels.ORDER_MIN_BYTES == 8 << 30
