@@ -56,14 +56,21 @@ against staged order, the sort's 0.11 ms included: every slot of a 262,144-slot 
 11.58 against 12.17 ms; 8 layers 2.86 against 3.02; 4 layers 1.52 against 1.53; 1 layer 0.47
 against 0.38 (the sort not repaid); a quarter of the cache's blocks, 32 layers, 3.12 against 3.08
 (writes spread over a sparse part of a cache gain nothing from order). The call cannot see the
-cache's size, so a call of this many slots into a cache several times larger sorts too, and can
-lose up to about 3 %: pass ``ordered=False`` there."""
+cache's size unless told it (``num_slots``), so a call of this many slots into a cache several
+times larger sorts too, and can lose up to about 3 %: pass ``num_slots`` or ``ordered=False``
+there."""
 
 
-def sort_first(n: int, layers: int, heads: int, d: int, elem: int, capturing: bool) -> bool:
+def sort_first(n: int, layers: int, heads: int, d: int, elem: int, capturing: bool,
+               num_slots: int | None = None) -> bool:
     """Whether :meth:`Kernels.scatter_rows` left to choose sorts its ``n`` pairs by slot first:
     from :data:`ORDER_MIN_SLOTS` slots and :data:`ORDER_MIN_BYTES` of rows, fewer than 2^31
-    pairs (the sort's limit), and not while the stream is being captured."""
+    pairs (the sort's limit), not while the stream is being captured, and, when the caller
+    names the cache's slot count, only when the call writes at least three quarters of the
+    cache (sorted writes gained 5 % over a whole cache and lost 1-3 % over a quarter or half
+    of one)."""
+    if num_slots is not None and 4 * n < 3 * num_slots:
+        return False
     return (not capturing and ORDER_MIN_SLOTS <= n < (1 << 31)
             and layers * heads * n * 2 * d * elem >= ORDER_MIN_BYTES)
 
@@ -409,6 +416,7 @@ class Kernels:
         strides: Sequence[int],
         elem_size: int,
         ordered: bool | None = None,
+        num_slots: int | None = None,
     ) -> None:
         """Write [L, H, cap, 2, d] rows back into the caches at ``slots`` and head slots ``heads``.
 
@@ -421,7 +429,9 @@ class Kernels:
         land either way. ``None`` sorts from :data:`ORDER_MIN_SLOTS` slots and
         :data:`ORDER_MIN_BYTES` of rows, where writing a whole cache through a permuted block
         table in slot order repays the sort, and never under graph capture (the sort clears its
-        counters with a memset, which a captured graph must not hold).
+        counters with a memset, which a captured graph must not hold). ``num_slots``, the
+        caches' slot count when the caller knows it, lets that choice see how much of the cache
+        the call writes (:func:`sort_first`).
         """
         import torch
 
@@ -436,7 +446,7 @@ class Kernels:
         with torch.cuda.device(slots.device):
             capturing = torch.cuda.is_current_stream_capturing()
             if ordered is None:
-                ordered = sort_first(n, nl, nh, int(d), int(elem_size), capturing)
+                ordered = sort_first(n, nl, nh, int(d), int(elem_size), capturing, num_slots)
             if ordered and capturing:
                 raise RuntimeError("scatter_rows: an ordered scatter cannot be captured in a graph "
                                    "(its sort clears counters with a memset)")
