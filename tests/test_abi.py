@@ -140,7 +140,7 @@ def test_scatter_rows_sorts_first_from_two_to_the_18_slots_and_8_gib():
     assert sf(1 << 18, layers=8, heads=8, d=128, elem=2, capturing=False)
     assert not sf(1 << 18, layers=4, heads=8, d=128, elem=2, capturing=False)
     assert kernels.ORDER_MIN_SLOTS == 1 << 18 and kernels.ORDER_MIN_BYTES == 8 << 30
-    # told the cache's slot count, it sorts only a call that writes three quarters of it or more
+    # told the cache's slot count, it sorts only a call that writes seven eighths of it or more
     assert sf(1 << 18, capturing=False, num_slots=1 << 18, **c4)
-    assert sf(3 << 18, capturing=False, num_slots=1 << 20, **c4)
-    assert not sf((3 << 18) - 1, capturing=False, num_slots=1 << 20, **c4)
+    assert sf(7 << 17, capturing=False, num_slots=1 << 20, **c4)
+    assert not sf((7 << 17) - 1, capturing=False, num_slots=1 << 20, **c4)
