@@ -121,6 +121,74 @@ class PagedKV:
             bad = lo if lo < 0 else hi
             raise ValueError(f"slot {bad} lies outside this cache's {self.num_slots} slots")
 
+    # The connector's row accessors (kvcopy.py:74-128), on the kernels: one launch each, on the
+    # current stream of the tensor's device. The connector indexes with torch, where a negative
+    # slot wraps to the cache's end; its callers never pass one (the snapshot clamps its slots
+    # first, mirror.py:579, and a restore writes stored ranges). Here a negative slot reads slot
+    # 0 and is not written, as the kernels treat padding.
+    def split(self, slots):
+        """Slot ids -> (block, offset in block), as int64 tensors."""
+        s = slots.long()
+        return s // self.block_size, s % self.block_size
+
+    def rows_of_heads(self, t, slots, heads):
+        """The K and V rows of head slots ``heads`` at ``slots``: a new ``[h, n, 2, d]`` tensor
+        (the connector returns a view of the same values)."""
+        import torch
+
+        n, h = int(slots.numel()), int(heads.numel())
+        out = torch.empty((1, h, n, 2, self.head_dim), dtype=t.dtype, device=t.device)
+        if n and h:
+            _kernels().gather_rows(_layer(t), _ids(slots, t), _ids(heads, t), out.data_ptr(), n,
+                                   self.head_dim, self.block_size, self.layout_strides(t),
+                                   t.element_size())
+        return out[0]
+
+    def rows(self, t, slots, head: int):
+        """The K and V rows of head slot ``head`` at ``slots``, as a copy ``[2, n, d]``."""
+        import torch
+
+        heads = torch.tensor([int(head)], dtype=torch.long, device=t.device)
+        return self.rows_of_heads(t, slots, heads)[0].transpose(0, 1).contiguous()
+
+    def write_rows(self, t, slots, head: int, x) -> None:
+        """Write ``x`` of shape ``[2, n, d]`` into head slot ``head`` at ``slots``, in place."""
+        import torch
+
+        n = int(slots.numel())
+        if tuple(x.shape) != (2, n, self.head_dim):
+            raise ValueError(f"write_rows: rows of shape {tuple(x.shape)}, expected "
+                             f"{(2, n, self.head_dim)}")
+        if x.dtype != t.dtype or x.device != t.device:
+            raise ValueError("write_rows: the rows must have the cache's dtype and device")
+        staged = x.transpose(0, 1).contiguous()  # [n, 2, d]: one layer, one head, capacity n
+        heads = torch.tensor([int(head)], dtype=torch.long, device=t.device)
+        if n:
+            _kernels().scatter_rows(_layer(t), _ids(slots, t), heads, staged.data_ptr(), n,
+                                    self.head_dim, self.block_size, self.layout_strides(t),
+                                    t.element_size(), ordered=False)
+
+
+def _kernels():
+    """The loaded kernels (raises when they cannot load: no quiet fallback)."""
+    from everserve_amd import kernels
+
+    return kernels.load()
+
+
+def _ids(ids, t):
+    """``ids`` as a contiguous int64 tensor on ``t``'s device."""
+    import torch
+
+    return ids.to(device=t.device, dtype=torch.long).contiguous()
+
+
+def _layer(t):
+    """A one-entry device table of ``t``'s address, as the kernels take layers."""
+    import torch
+
+    return torch.tensor([t.data_ptr()], dtype=torch.long, device=t.device)
+
 
 def strides_of(layout: CacheLayout | str, tensor_strides: Sequence[int],
                head_dim: int) -> tuple[int, int, int, int, int]:
