@@ -90,6 +90,15 @@ namespace {
 #ifndef EVS_GATHER_XCD_CHUNK
 #define EVS_GATHER_XCD_CHUNK 0
 #endif
+// A gather whose tiles cover every held head (one head group, as on a rank holding one KV head)
+// numbers its tiles along the slots alone, and there runs of 16 tiles per XCD (128 KiB of staged
+// rows each) beat round-robin. 7 interleaved rounds on each of two boxes: one bf16 head, 80
+// layers, 65,536 slots 6,184 / 6,218 against 5,946 / 5,978 GB/s (runs of 4 / 8 on the first:
+// 5,771 / 5,902); C3's fp8 head 6,138 / 6,216 against 6,030 / 6,131. With several head groups
+// the round-robin default stays (C2 6,078 against 6,074 under this switch's build).
+#ifndef EVS_GATHER_XCD_CHUNK_ONE_GROUP
+#define EVS_GATHER_XCD_CHUNK_ONE_GROUP 16
+#endif
 #ifndef EVS_SCATTER_XCD_CHUNK
 #define EVS_SCATTER_XCD_CHUNK 64
 #endif
@@ -562,6 +571,7 @@ int launch_typed(RowsArgs a, int64_t L, uint32_t W, hipStream_t stream, const ch
                 : I == kByRanges ? EVS_RANGES_XCD_CHUNK
                 : D == kGather ? EVS_GATHER_XCD_CHUNK : EVS_SCATTER_XCD_CHUNK;
   const int64_t groups = (a.H + a.HG - 1) / a.HG;
+  if (D == kGather && I != kByPairs && groups == 1) a.xcd_chunk = EVS_GATHER_XCD_CHUNK_ONE_GROUP;
   const int64_t per_slot = static_cast<int64_t>(a.HG) * 2 * W;
   int64_t ts = target / per_slot;
   ts = ts < 1 ? 1 : (ts > kMaxTileSlots ? kMaxTileSlots : ts);
