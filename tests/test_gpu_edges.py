@@ -146,6 +146,28 @@ def test_256_head_slots_in_one_call_and_257_refused(ext):
         assert live and all(np.array_equal(bits(a), bits(b)) for a, b in zip(dst, ref))
 
 
+@pytest.mark.parametrize("heads,n", [([1], 1024), ([1], 1025), ([1], 4807), ([2, 0], 1031),
+                                     ([2, 0], 4800)])
+def test_gathers_of_one_head_group_over_whole_and_partial_xcd_runs(ext, heads, n):
+    """A gather whose tiles cover every held head deals its tiles to the XCDs in runs (16 tiles
+    an XCD, 128 a round); a grid of exactly one round, one round and a few tiles, and several
+    rounds and a partial one, each byte against the oracle."""
+    nb, bs, layers_n = 1250, 4, 2
+    layers = caches("kv_first", 128, torch.bfloat16, n_layers=layers_n, nb=nb, bs=bs, h=H,
+                    seed=n)
+    slots = np.random.default_rng(n).choice(nb * bs, size=n, replace=False).astype(np.int64)
+    cap = n + 3
+    want = np.full((layers_n, len(heads), cap, 2, 128), SENTINEL, dtype=np.uint16)
+    oracle.gather_rows(layers, slots.tolist(), heads, cap, 128, bs, strides_of(layers[0]), 2,
+                       out=want)
+    gpu = [t.cuda() for t in layers]
+    out = torch.full(want.shape, SENTINEL, dtype=torch.int16, device="cuda")
+    ext.gather_rows(ptrs(gpu), dev_long(slots), dev_long(heads), out.data_ptr(), cap, 128, bs,
+                    list(strides_of(gpu[0])), 2)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy().view(np.uint16), want)
+
+
 @pytest.mark.parametrize("d", [8, 6])
 def test_the_gather_writes_straight_into_mapped_host_memory(ext, d):
     """Zero-copy, as the reference's staging does: out is host memory mapped for the device."""
