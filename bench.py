@@ -827,7 +827,7 @@ def bench_restore_host(ext, steps, warmup):
     import torch
 
     from everserve_amd.state.paged import PagedKV
-    from everserve_amd.state.restore import Restorer, Table, release_later
+    from everserve_amd.state.restore import Restorer, open_tables, release_later
 
     L, NB, BS, H, D = 4, 16384, 16, 8, 128
     n = NB * BS
@@ -865,7 +865,7 @@ def bench_restore_host(ext, steps, warmup):
         ours, release, opened, parts = [], [], [], []
         for _ in range(4):
             t0 = time.perf_counter()
-            tables = [Table.open(t, p, written) for t, p in paths.items()]
+            tables = open_tables((t, p, written) for t, p in paths.items())
             opened.append(time.perf_counter() - t0)
             rows = restorer.restore(tables, head_map)
             ours.append(time.perf_counter() - t0)
@@ -878,7 +878,7 @@ def bench_restore_host(ext, steps, warmup):
         release_s = sorted(release[1:])[1]
         payload = rows * row_bytes
         # a spare that mapped the tables ahead of the failure and keeps them mapped
-        tables = [Table.open(t, p, written) for t, p in paths.items()]
+        tables = open_tables((t, p, written) for t, p in paths.items())
         restorer.restore(tables, head_map)  # the pages' first touch
         ahead = []
         for _ in range(3):
@@ -925,8 +925,9 @@ def bench_restore_host(ext, steps, warmup):
                   f"at other head slots",
         "payload_bytes": payload,
         "tables_dir": os.path.dirname(tmp),
-        "timing": "4 restores each, every one opening the tables afresh inside its timing: the "
-                  "first cold, the steady state the median of the other 3. Ours is built "
+        "timing": "4 restores each, every one opening the tables afresh inside its timing (ours "
+                  "through open_tables, with Python's garbage collection paused as in the restore "
+                  "itself): the first cold, the steady state the median of the other 3. Ours is built "
                   "(restorer_build_ms) when the spare starts, before the first restore. Ours ends "
                   "when the cache is written; its tables' release is timed apart "
                   "(release_later). The reference's procedure releases each table inside its "
@@ -988,7 +989,7 @@ def bench_restore_catch_up(ext, steps, warmup):
     import numpy as np
     import torch
 
-    from everserve_amd.state.restore import Restorer, Table, release_later
+    from everserve_amd.state.restore import Restorer, open_tables, release_later
 
     L, NB, BS, H, D = 32, 16384, 16, 8, 128
     n = NB * BS
@@ -1000,9 +1001,10 @@ def bench_restore_catch_up(ext, steps, warmup):
     out = {"config": f"catch-up restore of {L * H} store tables ([262144, 2, 128] bf16) into a "
                      f"fresh 16384-block cache at other head slots: 64 sequences on a random "
                      f"block table, the slots written in the last S decode steps",
-           "timing": "4 restores each, tables mapped afresh inside each timing; cold = the "
-                     "first, steady = the median of the other 3; ours ends when the cache is "
-                     "written (the mappings are released after, apart)"}
+           "timing": "4 restores each, tables mapped afresh inside each timing (ours through "
+                     "open_tables, with Python's garbage collection paused); cold = the first, "
+                     "steady = the median of the other 3; ours ends when the cache is written (the "
+                     "mappings are released after, apart)"}
     shm = "/dev/shm" if os.path.isdir("/dev/shm") else None
     for since in (16, 256):
         slots, written = catch_up_written(since, num_blocks=NB, block_size=BS)
@@ -1029,7 +1031,7 @@ def bench_restore_catch_up(ext, steps, warmup):
             for _ in range(4):
                 torch.cuda.synchronize()
                 t0 = time.perf_counter()
-                tables = [Table.open(t, p, written) for t, p in paths.items()]
+                tables = open_tables((t, p, written) for t, p in paths.items())
                 opened.append(time.perf_counter() - t0)
                 got = restorer.restore(tables, head_map)
                 ours.append(time.perf_counter() - t0)
@@ -1041,7 +1043,7 @@ def bench_restore_catch_up(ext, steps, warmup):
             launches = restorer.timing.get("launches")
             # a spare that keeps the tables mapped from its first restore to the swap: the
             # catch-up then opens nothing and faults no page in
-            kept = [Table.open(t, p, written) for t, p in paths.items()]
+            kept = open_tables((t, p, written) for t, p in paths.items())
             restorer.restore(kept, head_map)
             mapped = []
             for _ in range(3):

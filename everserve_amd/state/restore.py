@@ -27,6 +27,8 @@ chunk: no slot ids are built or copied. Rows land byte for byte where ``write_ro
 
 from __future__ import annotations
 
+import contextlib
+import gc
 import mmap
 import os
 import threading
@@ -112,6 +114,44 @@ class Table:
         return cls(table, np.frombuffer(mapping, dtype=np.uint8), written)
 
 
+@contextlib.contextmanager
+def gc_paused():
+    """Python's automatic garbage collection off for the block, back on after if it was on: a
+    collection the block's allocations would set off runs after it instead. The switch is
+    process-wide: a thread that turns collection off meanwhile finds it on again when the block
+    ends."""
+    was = gc.isenabled()
+    gc.disable()
+    try:
+        yield
+    finally:
+        if was:
+            gc.enable()
+
+
+def open_tables(tables: Iterable[tuple[int, str, Sequence[tuple[int, int]]]]) -> list["Table"]:
+    """:meth:`Table.open` of each ``(table, path, written)``, with garbage collection paused."""
+    with gc_paused():
+        return [Table.open(t, path, written) for t, path, written in tables]
+
+
+def reserve_descriptors(count: int) -> None:
+    """Grow this process's file-descriptor table to hold ``count`` more descriptors than are open
+    now: hold that many duplicates of one descriptor at once, then close them (Linux never shrinks
+    the table)."""
+    if count <= 0:
+        return
+    fd = os.open(os.devnull, os.O_RDONLY)
+    held: list[int] = []
+    try:
+        for _ in range(count):
+            held.append(os.dup(fd))
+    finally:
+        for d in held:
+            os.close(d)
+        os.close(fd)
+
+
 def release_later(tables: list) -> threading.Thread:
     """Drop the restored ``tables`` (the list is emptied) on a daemon thread, so that unmapping
     their files, which costs about as much as restoring them, does not hold up the rank that
@@ -126,6 +166,29 @@ def release_later(tables: list) -> threading.Thread:
     th = threading.Thread(target=drop, daemon=True, name="everserve-restore-release")
     th.start()
     return th
+
+
+@dataclass
+class _Written:
+    """A written list's ranges as the plan uses them: the non-empty ranges' starts and counts
+    (an empty range writes nothing), whether any start or count is negative, the largest end
+    over every range, and the non-empty ranges as bytes, for grouping."""
+
+    source: Sequence[tuple[int, int]]
+    starts: np.ndarray
+    counts: np.ndarray
+    negative: bool
+    end: int
+    key: bytes
+
+    @classmethod
+    def of(cls, written: Sequence[tuple[int, int]]) -> "_Written":
+        w = np.asarray(written, dtype=np.int64).reshape(-1, 2)
+        starts, counts = w[:, 0], w[:, 1]
+        live = counts > 0
+        s, c = starts[live].copy(), counts[live].copy()
+        return cls(written, s, c, bool((starts < 0).any() or (counts < 0).any()),
+                   int((starts + counts).max()), s.tobytes() + c.tobytes())
 
 
 @dataclass
@@ -157,11 +220,20 @@ class Restorer:
     ``scales`` (optional): this rank's per-layer fp32 scale array on the device, ``[L]`` or
     ``[L, k]``, for an fp8 cache; :meth:`restore` writes the scales that travelled beside the rows
     into it. The rows themselves move as raw bytes and are never rescaled.
+
+    ``freeze_heap`` (default on): when built, the Restorer runs a full garbage collection and then
+    freezes every object left (``gc.freeze``), so that a later full collection walks only the
+    objects made since. A full collection walks every object the process holds, 40-70 ms on
+    MI355X hosts with torch loaded, and opening a restore's 256 tables allocates enough to set one
+    off: the first catch-up restore measured 40-63 ms of it in some runs and none in others. After
+    the freeze one takes well under a millisecond. Frozen objects are still freed when their last
+    reference goes, but a reference cycle among them is never collected: pass ``False`` to leave
+    the collector as it is.
     """
 
     def __init__(self, ext, layers: Sequence[torch.Tensor], chunk_bytes: int = 256 << 20,
                  threads: int | None = None, scales: torch.Tensor | None = None,
-                 piece_bytes: int = 64 << 20) -> None:
+                 piece_bytes: int = 64 << 20, freeze_heap: bool = True) -> None:
         first = layers[0]
         self._ext = ext
         self.layers = list(layers)
@@ -223,6 +295,15 @@ class Restorer:
         self._scattered: list[torch.cuda.Event | None] = [None, None]
         self.timing: dict[str, float] = {}
         self._lock = threading.Lock()  # one restore at a time owns the buffers and events
+        # A restore maps one table per (layer, head slot), and each mapping keeps a descriptor of
+        # its file open. Linux grows a process's descriptor table by doubling it, and in a process
+        # of more than one thread each growth waits for an RCU grace period: 15-40 ms a doubling
+        # on the hosts measured, so the first restore to hold 256 tables paid 50-90 ms in its opens. The table is
+        # grown now, at the spare's start (a few spare descriptors past one per table).
+        reserve_descriptors(len(layers) * most_heads + 16)
+        if freeze_heap:
+            gc.collect()
+            gc.freeze()
 
     def _head_list(self, heads: Sequence[int]) -> torch.Tensor:
         key = tuple(heads)
@@ -252,7 +333,11 @@ class Restorer:
         rb = self._row_bytes
         groups: dict[tuple, _Group] = {}
         taken: set[tuple[int, int]] = set()
-        ranges: dict[int, tuple[np.ndarray, np.ndarray]] = {}  # by the written list's identity
+        # What a written list yields, worked out once per list (a store commit hands every table
+        # of a step the same one): the catch-up after 16 decode steps checks 256 tables of 125
+        # ranges each, which took 3.8 ms table by table and takes 0.8 ms with the list's work
+        # done once (one x86 host).
+        ranges: dict[int, _Written] = {}  # by the written list's identity
         for table in tables:
             if table.head not in head_map or not table.written:
                 continue
@@ -273,25 +358,20 @@ class Restorer:
             rows = table.rows
             if rows.nbytes % rb or (rows.ndim == 2 and rows.shape[1] * rows.itemsize != rb):
                 raise ValueError(f"{name}: not a whole number of this cache's {rb}-byte rows")
-            got = ranges.get(id(table.written))
-            if got is None or got[2] is not table.written:
-                w = np.asarray(table.written, dtype=np.int64).reshape(-1, 2)
-                got = ranges[id(table.written)] = (w[:, 0].copy(), w[:, 1].copy(), table.written)
-            starts, counts = got[0], got[1]
-            ends = starts + counts
-            if (starts < 0).any() or (counts < 0).any() or ends.max() > rows.nbytes // rb:
+            w = ranges.get(id(table.written))
+            if w is None or w.source is not table.written:
+                w = ranges[id(table.written)] = _Written.of(table.written)
+            if w.negative or w.end > rows.nbytes // rb:
                 raise ValueError(f"{name}: a written range lies outside the table")
-            if ends.max() > geo.num_slots:
-                raise ValueError(f"{name}: a written range ends at slot {int(ends.max())}, past "
+            if w.end > geo.num_slots:
+                raise ValueError(f"{name}: a written range ends at slot {w.end}, past "
                                  f"this cache's {geo.num_slots} slots")
-            live = counts > 0  # an empty range writes nothing
-            starts, counts = starts[live], counts[live]
-            if not len(starts):
+            if not len(w.starts):
                 continue
-            key = (layer, starts.tobytes(), counts.tobytes(), rows.nbytes)
+            key = (layer, w.key, rows.nbytes)
             g = groups.get(key)
             if g is None:
-                g = groups[key] = _Group([layer], starts, counts, [], [])
+                g = groups[key] = _Group([layer], w.starts, w.counts, [], [])
             g.tables.append(table)
             g.heads.append(head)
         return self._merge(list(groups.values()))
@@ -332,9 +412,10 @@ class Restorer:
         Every table is checked first (:meth:`plan`); a refused restore writes nothing. Returns the
         rows written, over every table. Synchronises the device at the end, as the reference's
         restore does (core/everserve/state/mirror.py:938-939). Restores through one Restorer from
-        several threads run one after another: they share its buffers.
+        several threads run one after another: they share its buffers. Python's automatic garbage
+        collection is paused while it runs (:func:`gc_paused`).
         """
-        with self._lock:
+        with self._lock, gc_paused():
             return self._restore(tables, head_map, scales)
 
     def _restore(self, tables: Iterable[Table], head_map: Mapping[int, int],

@@ -66,3 +66,64 @@ def test_release_later_drops_the_tables_off_the_calling_thread(tmp_path):
     th.join()
     gc.collect()
     assert all(m() is None for m in maps)
+
+
+def test_written_ranges_are_summarised_once_as_the_plan_reads_them():
+    """The plan's view of a written list: empty ranges dropped, any negative start or count
+    flagged, the largest end over every range (empty ones included)."""
+    from everserve_amd.state.restore import _Written
+
+    w = _Written.of([(4, 3), (9, 0), (12, 5), (40, 0)])
+    assert w.starts.tolist() == [4, 12] and w.counts.tolist() == [3, 5]
+    assert not w.negative and w.end == 40
+    assert w.key == _Written.of([(4, 3), (12, 5)]).key
+    assert w.key != _Written.of([(4, 3), (12, 6)]).key
+    assert _Written.of([(-1, 2)]).negative and _Written.of([(3, -1)]).negative
+    assert _Written.of([(0, 0)]).starts.size == 0
+
+
+def test_reserving_descriptors_grows_the_table_and_leaves_none_open():
+    """reserve_descriptors holds its duplicates only while it runs; the descriptor table then
+    has room for that many more."""
+    import os
+
+    from everserve_amd.state.restore import reserve_descriptors
+
+    def fdsize() -> int:
+        with open("/proc/self/status") as f:
+            return next(int(line.split()[1]) for line in f if line.startswith("FDSize"))
+
+    before = sorted(os.listdir("/proc/self/fd"))
+    reserve_descriptors(600)
+    reserve_descriptors(0)
+    assert sorted(os.listdir("/proc/self/fd")) == before
+    assert fdsize() >= len(before) + 600
+
+
+def test_gc_paused_restores_the_collector_as_it_found_it(tmp_path):
+    """Collection is off inside the block and as before after it, also when the block raises;
+    open_tables opens every table inside such a block."""
+    import gc
+
+    from everserve_amd.state.restore import gc_paused, open_tables
+
+    assert gc.isenabled()
+    with gc_paused():
+        assert not gc.isenabled()
+    assert gc.isenabled()
+    with pytest.raises(RuntimeError):
+        with gc_paused():
+            raise RuntimeError("inside")
+    assert gc.isenabled()
+    gc.disable()
+    try:
+        with gc_paused():
+            pass
+        assert not gc.isenabled()
+    finally:
+        gc.enable()
+    path = tmp_path / "t.rows"
+    path.write_bytes(bytes(range(64)) * 4)
+    tables = open_tables([(3, str(path), [(0, 2)]), (1004, str(path), [(1, 1)])])
+    assert [t.table for t in tables] == [3, 1004] and tables[1].head == 4
+    assert tables[0].rows.nbytes == 256 and bytes(tables[0].rows[:4]) == bytes(range(4))
