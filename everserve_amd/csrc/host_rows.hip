@@ -33,7 +33,11 @@
 namespace evs {
 namespace {
 
-constexpr int64_t kMinBytesPerThread = int64_t{4} << 20;  // below this a thread costs more than it copies
+// A gather of fewer bytes than this a thread runs on fewer threads. Table pages mapped afresh
+// fault in as they are read (about 30 GB/s on 16 threads, where warm pages copy at 100 and more),
+// so a thread is worth waking for 1 MiB: with 4 MiB a thread, the restore's 16 MiB pieces ran on
+// 4 threads and a catch-up of 256 tables took 15 ms instead of 7.
+constexpr int64_t kMinBytesPerThread = int64_t{1} << 20;
 
 void copy_bytes(char* dst, const char* src, size_t bytes) {
   if (EVS_HOST_NT_STORES)

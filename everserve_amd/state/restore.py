@@ -209,13 +209,16 @@ class Restorer:
     """Writes restored tables into ``layers`` (this rank's caches, in layer order).
 
     ``chunk_bytes`` is the rows one scatter launch writes over all of a group's tables, and
-    ``piece_bytes`` the rows one host gather and one copy to the device carry; two pinned and two
-    device buffers of ``chunk_bytes`` are allocated, and the pinned ones touched, once, here: a
-    spare builds its Restorer when it starts, before any failure. On MI355X, inside a restore from
-    ``/dev/shm``, a scatter of 64 MiB ran at 4.9 TB/s, of 128 MiB at 5.4 and of 256 MiB at 5.7
-    (a launch's ramp and tail weigh on the shorter ones), while the restore as a whole, bound by
-    the PCIe copies, ran 0.5-1 % slower with 256 MiB copies than with 64 MiB ones, which fill and
-    drain the pipeline sooner: hence large chunks of small pieces.
+    ``piece_bytes`` the most rows one host gather and one copy to the device carry (a group is
+    cut into at least 8 pieces of 16 MiB or more); two pinned and two device buffers of
+    ``chunk_bytes`` are allocated, and the pinned ones touched, once, here: a spare builds its
+    Restorer when it starts, before any failure. On MI355X, inside a restore from ``/dev/shm``, a
+    scatter of 64 MiB ran at 4.9 TB/s, of 128 MiB at 5.4 and of 256 MiB at 5.7 (a launch's ramp
+    and tail weigh on the shorter ones), while the restore as a whole, bound by the PCIe copies,
+    ran 0.5-1 % slower with 256 MiB copies than with 64 MiB ones, which fill and drain the
+    pipeline sooner: hence large chunks of small pieces. A catch-up's groups are small (128 MiB
+    for every table after 16 decode steps): there 16 MiB pieces took 6.4-6.8 ms against 6.9-7.1
+    with 64 MiB ones, and the first catch-up after 256 steps 45 ms against 48-49.
 
     ``scales`` (optional): this rank's per-layer fp32 scale array on the device, ``[L]`` or
     ``[L, k]``, for an fp8 cache; :meth:`restore` writes the scales that travelled beside the rows
@@ -480,7 +483,10 @@ class Restorer:
         srcs = [t.rows.ctypes.data for t in g.tables]
         table_rows = g.tables[0].rows.nbytes // rb
         per_chunk = max(1, self._chunk_bytes // (k * rb))
-        per_piece = max(1, self._piece_bytes // (k * rb))
+        # at least 8 pieces a group, of 16 MiB or more: the pipeline's fill (the first piece's
+        # gather) and drain (the last piece's copy) are then a small part of a small group too
+        piece = min(self._piece_bytes, max(16 << 20, rows * k * rb // 8))
+        per_piece = max(1, piece // (k * rb))
         if k * per_chunk * rb > self._chunk_bytes:
             raise RuntimeError(f"layer {layer}: a chunk of {k} tables x {per_chunk} rows does "
                                f"not fit the {self._chunk_bytes}-byte buffers")
