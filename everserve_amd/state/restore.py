@@ -138,14 +138,18 @@ def open_tables(tables: Iterable[tuple[int, str, Sequence[tuple[int, int]]]]) ->
 def reserve_descriptors(count: int) -> None:
     """Grow this process's file-descriptor table to hold ``count`` more descriptors than are open
     now: hold that many duplicates of one descriptor at once, then close them (Linux never shrinks
-    the table)."""
+    the table). It stops early, without an error, at the process's descriptor limit: the growth
+    only saves time."""
     if count <= 0:
         return
     fd = os.open(os.devnull, os.O_RDONLY)
     held: list[int] = []
     try:
         for _ in range(count):
-            held.append(os.dup(fd))
+            try:
+                held.append(os.dup(fd))
+            except OSError:
+                break
     finally:
         for d in held:
             os.close(d)

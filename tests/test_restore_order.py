@@ -100,6 +100,24 @@ def test_reserving_descriptors_grows_the_table_and_leaves_none_open():
     assert fdsize() >= len(before) + 600
 
 
+def test_reserving_past_the_descriptor_limit_stops_there_quietly():
+    """At the process's descriptor limit the reservation stops without an error and closes
+    what it held."""
+    import os
+    import resource
+
+    from everserve_amd.state.restore import reserve_descriptors
+
+    soft, hard = resource.getrlimit(resource.RLIMIT_NOFILE)
+    before = sorted(os.listdir("/proc/self/fd"))
+    resource.setrlimit(resource.RLIMIT_NOFILE, (len(before) + 40, hard))
+    try:
+        reserve_descriptors(500)
+    finally:
+        resource.setrlimit(resource.RLIMIT_NOFILE, (soft, hard))
+    assert sorted(os.listdir("/proc/self/fd")) == before
+
+
 def test_gc_paused_restores_the_collector_as_it_found_it(tmp_path):
     """Collection is off inside the block and as before after it, also when the block raises;
     open_tables opens every table inside such a block."""
