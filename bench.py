@@ -645,7 +645,8 @@ def host_numa():
 def c3_stager_round(ext, layers, blocks, dev):
     """C3's 2048 blocks as one notice round through the product's StepStager: the block gather,
     then the delivery into the stage's file. Timed from commit until the sink has the file,
-    three rounds (the first creates and faults in the file; the median of the other two)."""
+    three rounds (the median of the last two), after ``prepare`` made the round's file and
+    buffers (timed apart); then one round of another size, whose file the first commit makes."""
     import torch
 
     from everserve_amd.state.staging import StepStager
@@ -653,18 +654,31 @@ def c3_stager_round(ext, layers, blocks, dev):
     kv = {f"model.layers.{i}.self_attn.attn": t for i, t in enumerate(layers)}
     scales = torch.ones(len(layers), dtype=torch.float32, device=dev)
     times = []
+    ids = blocks.tolist()
+    bs = layers[0].shape[2]
     with StepStager(ext, kv, [0], lambda job: None, scales=scales) as st:
+        t0 = time.perf_counter()
+        st.prepare([len(ids) * bs])
+        prepare_s = time.perf_counter() - t0
         for k in range(3):
             torch.cuda.synchronize()
             t0 = time.perf_counter()
-            n = st.commit_blocks(1, k + 1, blocks.tolist())
+            n = st.commit_blocks(1, k + 1, ids)
             st.flush()
             times.append(time.perf_counter() - t0)
+        half = ids[:len(ids) // 2]  # another capacity: no file of its size in the pool
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        st.commit_blocks(1, 4, half)
+        st.flush()
+        unprepared_s = time.perf_counter() - t0
         bounce_nodes = page_nodes([b.data_ptr() for b in st._bounce], st._bounce_bytes)
     payload = n * len(layers) * layers[0].shape[-1] * 2
     ms = sorted(times[1:])[0] * 1e3
-    return {"first_ms": round(times[0] * 1e3, 3), "ms": round(ms, 3),
-            "gbs": round(payload / ms / 1e6, 2), "repeats_ms": [round(t * 1e3, 2) for t in times],
+    return {"prepare_ms": round(prepare_s * 1e3, 3), "first_ms": round(times[0] * 1e3, 3),
+            "ms": round(ms, 3), "gbs": round(payload / ms / 1e6, 2),
+            "repeats_ms": [round(t * 1e3, 2) for t in times],
+            "half_round_unprepared_ms": round(unprepared_s * 1e3, 3),
             "bounce_numa_nodes": bounce_nodes}
 
 

