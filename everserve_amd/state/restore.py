@@ -192,7 +192,7 @@ class _Written:
         live = counts > 0
         s, c = starts[live].copy(), counts[live].copy()
         return cls(written, s, c, bool((starts < 0).any() or (counts < 0).any()),
-                   int((starts + counts).max()), s.tobytes() + c.tobytes())
+                   int((starts + counts).max()) if len(w) else 0, s.tobytes() + c.tobytes())
 
 
 @dataclass

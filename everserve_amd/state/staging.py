@@ -368,8 +368,8 @@ class StepStager:
         round after it took 14.4 ms (13.1 steady), where an unprepared first round took 109 ms.
         The pool keeps ``depth + 1`` of them; more are made and dropped again."""
         for n in slot_counts:
-            if int(n) < 0:
-                raise ValueError(f"a step of {n} slots")
+            if int(n) < 1:
+                raise ValueError(f"a step stages at least one slot, not {n} slots")
             self._release(self._staging(int(n)))
 
     # ---------------------------------------------------------------- the step thread

@@ -80,6 +80,7 @@ def test_written_ranges_are_summarised_once_as_the_plan_reads_them():
     assert w.key != _Written.of([(4, 3), (12, 6)]).key
     assert _Written.of([(-1, 2)]).negative and _Written.of([(3, -1)]).negative
     assert _Written.of([(0, 0)]).starts.size == 0
+    assert _Written.of([]).end == 0 and not _Written.of([]).negative
 
 
 def test_reserving_descriptors_grows_the_table_and_leaves_none_open():
