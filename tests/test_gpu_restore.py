@@ -395,3 +395,36 @@ def test_layers_with_the_same_ranges_share_a_launch_unless_heads_or_layout_diffe
                 rest = oracle.gather_rows([cpu], list(range(nb * bs)), [0], nb * bs, d, bs,
                                           strides_of(cpu), 2)
                 assert not rest.any()
+
+
+def test_a_catch_up_sized_group_in_16_mib_pieces(ext):
+    """8 tables of 16 MiB whose written ranges are 630 runs of 24-48 rows (about 90 MiB over the
+    group): the Restorer cuts the group into pieces of 16 MiB, ranges cut at the pieces' edges,
+    one launch for the chunk. Every row lands where torch's indexing puts it (the tables' rows at
+    their slots, head by head), and nothing else is written."""
+    nb, bs, h, d = 2048, 16, 8, 128
+    n = nb * bs
+    rng = np.random.default_rng(7)
+    starts = np.arange(630) * 52 + rng.integers(0, 4, size=630)
+    counts = rng.integers(24, 49, size=630)
+    written = [(int(s), int(c)) for s, c in zip(starts, counts)]
+    assert 5 * (16 << 20) < int(counts.sum()) * h * 512 < 7 * (16 << 20)
+    tables = {}
+    for head in range(h):
+        rows = rng.integers(0, 1 << 16, size=(n, 2 * d), dtype=np.uint16) & 0xBFFF
+        tables[head] = rows.view(np.uint8)
+    dst = torch.zeros((2, nb, bs, h, d), dtype=torch.bfloat16, device="cuda")
+    r = Restorer(ext, [dst])
+    moves = {x: (x + 3) % h for x in range(h)}
+    got = r.restore([Table(x, tables[x], written) for x in range(h)], moves)
+    slots = np.concatenate([np.arange(s, s + c) for s, c in written])
+    assert got == slots.size * h
+    assert r.timing["launches"] == 1
+    want = torch.zeros_like(dst)
+    s = torch.from_numpy(slots).cuda()
+    for x in range(h):
+        rows = torch.from_numpy(tables[x].view(np.int16).reshape(n, 2, d)).cuda()
+        want[:, s // bs, s % bs, moves[x]] = rows[s].transpose(0, 1).contiguous().view(
+            torch.bfloat16)
+    torch.cuda.synchronize()
+    assert torch.equal(dst.view(torch.int16), want.view(torch.int16))
