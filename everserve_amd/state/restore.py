@@ -213,8 +213,8 @@ class Restorer:
     """Writes restored tables into ``layers`` (this rank's caches, in layer order).
 
     ``chunk_bytes`` is the rows one scatter launch writes over all of a group's tables, and
-    ``piece_bytes`` the most rows one host gather and one copy to the device carry (a group is
-    cut into at least 8 pieces of 16 MiB or more); two pinned and two device buffers of
+    ``piece_bytes`` the most rows one host gather and one copy to the device carry (a piece is
+    an eighth of its group, but 16 MiB at least); two pinned and two device buffers of
     ``chunk_bytes`` are allocated, and the pinned ones touched, once, here: a spare builds its
     Restorer when it starts, before any failure. On MI355X, inside a restore from ``/dev/shm``, a
     scatter of 64 MiB ran at 4.9 TB/s, of 128 MiB at 5.4 and of 256 MiB at 5.7 (a launch's ramp
@@ -305,8 +305,9 @@ class Restorer:
         # A restore maps one table per (layer, head slot), and each mapping keeps a descriptor of
         # its file open. Linux grows a process's descriptor table by doubling it, and in a process
         # of more than one thread each growth waits for an RCU grace period: 15-40 ms a doubling
-        # on the hosts measured, so the first restore to hold 256 tables paid 50-90 ms in its opens. The table is
-        # grown now, at the spare's start (a few spare descriptors past one per table).
+        # on the hosts measured, so the first restore to hold 256 tables paid 50-90 ms in its
+        # opens. The table is grown now, at the spare's start (a few spare descriptors past one
+        # per table).
         reserve_descriptors(len(layers) * most_heads + 16)
         if freeze_heap:
             gc.collect()
@@ -487,8 +488,9 @@ class Restorer:
         srcs = [t.rows.ctypes.data for t in g.tables]
         table_rows = g.tables[0].rows.nbytes // rb
         per_chunk = max(1, self._chunk_bytes // (k * rb))
-        # at least 8 pieces a group, of 16 MiB or more: the pipeline's fill (the first piece's
-        # gather) and drain (the last piece's copy) are then a small part of a small group too
+        # pieces of an eighth of the group, but 16 MiB at least and piece_bytes at most: the
+        # pipeline's fill (the first piece's gather) and drain (the last piece's copy) are then a
+        # small part of a small group too
         piece = min(self._piece_bytes, max(16 << 20, rows * k * rb // 8))
         per_piece = max(1, piece // (k * rb))
         if k * per_chunk * rb > self._chunk_bytes:
