@@ -29,8 +29,13 @@
 // the unrun path's code slowed the all-in call.
 //
 // The call's outcome is one word, state[0] = (epoch << 16) | (reason << 8) | late rows, written by
-// the last workgroup to count. Each workgroup counts once its wait is over, before its payload:
-// the outcome is settled then, and state[0] is read only after the kernel has completed. How a
+// the last workgroup to count. Each workgroup counts once its wait is over: the outcome is settled
+// then, and state[0] is read only after the kernel has completed. The counting runs in a wave of
+// its own after the payload's (EVS_REDUCE_CONTROL_WAVE), which moves no payload: a wave's memory
+// operations complete in issue order, so in a payload wave each counting atomic held that wave's
+// first sum until it returned, and the last of a word's serialised atomics held the call (on
+// MI355X the control wave took C5 from 9.34 to 9.02 us a call, 16 Ki elements from 3.16 to 2.98,
+// 64 Ki from 3.21 to 2.96, and a grid of one, whose outcome store it also takes, 2.94 to 2.78). How a
 // call counts depends on its grid, and is a template parameter chosen at launch, so each kernel
 // holds only its own mode's code (on MI355X the code of modes a call does not run cost a small
 // grid 0.2-0.3 us, through the registers and schedule of its payload loop):
@@ -46,9 +51,9 @@
 //     workgroup cost 2.8 us of a 13 us call at 256 workgroups).
 // No fence is needed, so no workgroup writes back or invalidates the L2. The counting words return
 // to zero at the end of every call, so the launch needs no memset and a captured graph can replay
-// it. These atomics run in one lane and their answers are read late; the file is built without
-// the compiler's atomic optimizer, whose wave-wide form of them would read each answer at once
-// and so wait out the round trip in front of the payload loads.
+// it. These atomics run in one lane; the file is built without the compiler's atomic optimizer,
+// whose wave-wide form of them would read each answer at once (with the control wave off, that
+// waited out the round trip in front of the payload loads).
 
 #include "common.hpp"
 
@@ -62,16 +67,25 @@ namespace {
 #ifndef EVS_REDUCE_NT
 #define EVS_REDUCE_NT 3
 #endif
-constexpr int kThreads = EVS_REDUCE_THREADS;
+constexpr int kThreads = EVS_REDUCE_THREADS;  // the threads that move the payload
+// 1: each workgroup has one more wave, after the payload's, that does the completion counting. A
+// wave's memory operations complete in the order they were issued, so a counting atomic issued by
+// a payload wave holds that wave's first sum until the atomic returns, and the atomics of one
+// counting word are serialised: the last of a group's arrivals cost the call its wait.
+#ifndef EVS_REDUCE_CONTROL_WAVE
+#define EVS_REDUCE_CONTROL_WAVE 1
+#endif
+constexpr bool kControl = EVS_REDUCE_CONTROL_WAVE != 0;
+constexpr int kBlockThreads = kThreads + (kControl ? 64 : 0);
 constexpr int kMaxRows = EVS_MAX_ROWS;
 #ifndef EVS_REDUCE_VPT
 #define EVS_REDUCE_VPT 4
 #endif
-// At most two workgroups a CU: the 4-vector kernel's registers leave room for two waves a SIMD, so
-// every workgroup of the largest grid is resident at once and each waits out its own bounded wait
-// (a grid past that would time out in turns).
+// Every workgroup of the largest grid is resident at once, so that each waits out its own bounded
+// wait (a grid past that would time out in turns). The 4-vector kernel's registers leave room for
+// two waves a SIMD: two workgroups of 4 waves a CU, one of 5 with the control wave.
 #ifndef EVS_REDUCE_MAX_BLOCKS
-#define EVS_REDUCE_MAX_BLOCKS 512
+#define EVS_REDUCE_MAX_BLOCKS (EVS_REDUCE_CONTROL_WAVE ? 256 : 512)
 #endif
 constexpr int kMaxVpt = EVS_REDUCE_VPT;  // 8-element vectors per thread per pass, at most
 constexpr int kMaxBlocks = EVS_REDUCE_MAX_BLOCKS;  // all resident on 256 CUs
@@ -338,7 +352,7 @@ __device__ __forceinline__ void sum_store(const u32x4 (&x)[V][kMaxRows],
 
 // The rest of a call from vector vb on: the passes of the vector path, the elements the vectors
 // do not cover, and the completion count (in counting mode C).
-template <int V, int C>
+template <int V, int C, bool kCounting = !kControl>
 __device__ __forceinline__ void finish_call(const ReduceArgs& a,
                                             const uint16_t* const (&src)[kMaxRows], int count,
                                             int64_t nvec, int64_t vb, uint64_t* group_word,
@@ -350,7 +364,7 @@ __device__ __forceinline__ void finish_call(const ReduceArgs& a,
   // It does so right after its first pass's loads are issued: its wait for the group word's
   // answer (counted before the payload) then leaves those loads in flight, and the top word's
   // answer is only read at the end, so no atomic round trip is left for the end of the call.
-  constexpr bool two_level = C == kCountTwoLevel;
+  constexpr bool two_level = kCounting && C == kCountTwoLevel;
   bool top_sent = false, group_last = false;
   uint64_t group_all = 0, top_before = 0;
   // vectors of 8 elements: one 16-byte load per member
@@ -433,7 +447,7 @@ __device__ __forceinline__ void finish_call(const ReduceArgs& a,
     a.out[e] = static_cast<uint16_t>(f32_to_bf16(acc));
   }
 
-  if (tid == 0) {
+  if (kCounting && tid == 0) {
     uint64_t outcome = own_outcome;
     bool all_in = true;  // this workgroup has every workgroup's outcome in `outcome`
     if (two_level) {
@@ -452,8 +466,31 @@ __device__ __forceinline__ void finish_call(const ReduceArgs& a,
   }
 }
 
+// The control wave's counting, in its lane 0: this workgroup's arrival with outcome `own`, as
+// finish_call counts it in the payload's first wave, and for the call's last arrival the outcome
+// word. Its wave issues nothing else, so each atomic's answer waits behind no payload load, and
+// the chain ends long before the payload does.
+template <int C>
+__device__ __forceinline__ void count_arrival(const ReduceArgs& a, uint64_t* group_word,
+                                              uint32_t group, uint32_t groups, uint64_t own) {
+  uint64_t outcome = own;
+  bool all_in = true;  // this arrival has every workgroup's outcome in `outcome`
+  if (C == kCountTwoLevel) {
+    const uint64_t before = arrive(group_word, own);
+    const uint32_t in_group = (gridDim.x - group + groups - 1) / groups;  // b % groups == group
+    uint64_t group_all = 0;
+    all_in = last(group_word, before, in_group, group_all);
+    if (all_in) all_in = last(a.state + 1, arrive(a.state + 1, group_all), groups, outcome);
+  } else if (C == kCountFlat) {
+    all_in = last(group_word, arrive(group_word, own), gridDim.x, outcome);  // the top word
+  }
+  if (all_in)
+    __hip_atomic_store(a.state + 0, (a.epoch << 16) | outcome, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 template <int V, int C>
-__global__ __launch_bounds__(kThreads) void local_reduce(ReduceArgs a) {
+__global__ __launch_bounds__(kBlockThreads) void local_reduce(ReduceArgs a) {
   constexpr bool kStartsEarly = EVS_REDUCE_EARLY && V >= EVS_REDUCE_EARLY_MIN_VPT;
   __shared__ const uint16_t* s_src[kMaxRows];  // member in order position q, or null: missing
   __shared__ int s_count;
@@ -524,7 +561,14 @@ __global__ __launch_bounds__(kThreads) void local_reduce(ReduceArgs a) {
   uint64_t group_before = 0;
   const int mode = s_mode;
   const bool waiting = kStartsEarly && (mode & kEarly) != 0;
-  if (tid == 0 && !waiting && counts) group_before = arrive(group_word, s_outcome);
+  if constexpr (kControl) {
+    if (tid >= kThreads) {  // the control wave: it counts, and moves no payload
+      if (waiting) __syncthreads();  // the early start's barrier, after wave 0's wait
+      if (tid == kThreads) count_arrival<C>(a, group_word, group, groups, s_outcome);
+      return;
+    }
+  }
+  if (!kControl && tid == 0 && !waiting && counts) group_before = arrive(group_word, s_outcome);
 
   const int count = s_count;
   const int64_t nvec = (mode & kVectors) ? a.nvec : 0;
@@ -563,7 +607,7 @@ __global__ __launch_bounds__(kThreads) void local_reduce(ReduceArgs a) {
         }
       }
       __syncthreads();
-      if (tid == 0 && counts) group_before = arrive(group_word, s_outcome);
+      if (!kControl && tid == 0 && counts) group_before = arrive(group_word, s_outcome);
       load_late(x, s_late, __builtin_amdgcn_readfirstlane(s_came), vb, records, tid);
       sum_store(x, uniform_rsrc(a.out + vb * 8, records), tid);
       vb += static_cast<int64_t>(gridDim.x) * kThreads * V;
@@ -652,7 +696,7 @@ extern "C" int evs_local_reduce(const int64_t* bufs, const uint64_t* flags, cons
   if (tail_blocks > blocks) blocks = tail_blocks;
   if (blocks < 1) blocks = 1;
   if (blocks > evs::kMaxBlocks) blocks = evs::kMaxBlocks;
-  const dim3 grid(static_cast<uint32_t>(blocks)), block(evs::kThreads);
+  const dim3 grid(static_cast<uint32_t>(blocks)), block(evs::kBlockThreads);
   hipStream_t s = evs::as_stream(stream);
   // The counting mode follows the grid. Two-level counting is right for any grid, so the wider
   // kernels, whose grids are past the flat bound whenever the rule above picks them, carry only it.
