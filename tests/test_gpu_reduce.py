@@ -101,6 +101,23 @@ def test_the_sum_is_the_ordered_fp32_sum_bit_for_bit(ext, n, order):
     assert not m.state[1:].any()  # the kernel's counters are back at zero
 
 
+@pytest.mark.parametrize("n", [3 * (1 << 20) + 5, 6 * (1 << 20)])
+def test_calls_past_the_resident_grid_take_several_passes(ext, n):
+    """Past 2 Mi elements the 4-vector kernel's grid stays at 256 workgroups, one a CU with the
+    counting wave beside the payload's, so each workgroup takes several passes: the sum is still
+    the ordered fp32 sum bit for bit, the outcome is counted once, the counters end at zero."""
+    order = [6, 1, 4, 0, 3, 7, 2, 5]
+    inputs = {r: bf16_input(300 + r, n) for r in order}
+    m = Members(inputs, order)
+    m.publish(epoch=2)
+    ext.local_reduce(m.bufs, m.flags, m.order, m.out, 2, 10**9, 0, m.state)
+    torch.cuda.synchronize()
+    want = oracle.member_sum([bits(inputs[r]) for r in order])
+    assert np.array_equal(bits(m.out), want)
+    assert m.status() == (2, 0, 0)
+    assert not m.state[1:].any()
+
+
 def test_the_order_of_the_sum_shows_and_is_kept(ext):
     n = 16384
     g = torch.Generator().manual_seed(7)
