@@ -50,8 +50,8 @@
 //     of the atomics, which on MI355X serialise per address at device scope (one word for every
 //     workgroup cost 2.8 us of a 13 us call at 256 workgroups).
 // No fence is needed, so no workgroup writes back or invalidates the L2. The counting words return
-// to zero at the end of every call, so the launch needs no memset and a captured graph can replay
-// it. These atomics run in one lane; the file is built without the compiler's atomic optimizer,
+// to zero in every call, once its last arrival is counted, so the launch needs no memset and a
+// captured graph can replay it. These atomics run in one lane; the file is built without the compiler's atomic optimizer,
 // whose wave-wide form of them would read each answer at once (with the control wave off, that
 // waited out the round trip in front of the payload loads).
 
