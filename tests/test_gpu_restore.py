@@ -428,3 +428,17 @@ def test_a_catch_up_sized_group_in_16_mib_pieces(ext):
             torch.bfloat16)
     torch.cuda.synchronize()
     assert torch.equal(dst.view(torch.int16), want.view(torch.int16))
+
+
+def test_the_heap_is_frozen_when_built_unless_asked_not_to(ext):
+    """freeze_heap (default on) collects and freezes the Python heap when the Restorer is built;
+    freeze_heap=False leaves the collector as it is. Either way the collector is on afterwards."""
+    import gc
+
+    dst = [torch.zeros((2, 8, 4, 2, 8), dtype=torch.bfloat16, device="cuda")]
+    gc.unfreeze()
+    Restorer(ext, dst, freeze_heap=False)
+    assert gc.get_freeze_count() == 0 and gc.isenabled()
+    Restorer(ext, dst)
+    assert gc.get_freeze_count() > 0 and gc.isenabled()
+    gc.unfreeze()
