@@ -645,8 +645,9 @@ def host_numa():
 def c3_stager_round(ext, layers, blocks, dev):
     """C3's 2048 blocks as one notice round through the product's StepStager: the block gather,
     then the delivery into the stage's file. Timed from commit until the sink has the file,
-    three rounds (the median of the last two), after ``prepare`` made the round's file and
-    buffers (timed apart); then one round of another size, whose file the first commit makes."""
+    three rounds (the faster of the last two reported), after ``prepare`` made the round's file
+    and buffers (timed apart); then one round of another size, whose file the first commit
+    makes."""
     import torch
 
     from everserve_amd.state.staging import StepStager
